@@ -1,0 +1,274 @@
+"""Benchmark of the batched-FFT hot path on one MI355X; prints ONE JSON line.
+
+Workload ("C1"): batched complex64 C2C, n = 1024, batch = 16384
+(2^24 points), real and imaginary parts U[-1, 1) from a fixed seed (synthetic data). One step is
+a forward transform plus an inverse transform (impl "stockham_r8" unless --impl says otherwise),
+called through the C ABI (libspectral_hip.so) on one HIP stream.
+
+value        effective HBM GB/s of the step: algorithmic bytes (16 B per point per direction,
+             reference csrc/common/bench.cpp:93-100) / wall time of the timed steps.
+roofline     the forward C2C kernel alone: the same algorithmic bytes per launch / its average
+             launch time measured with HIP events on the stream it runs on; peak = 8000 GB/s.
+             `traffic` (HBM bytes per launch from rocprof FETCH_SIZE + WRITE_SIZE) is filled in
+             from profiles/ when a counter summary for this kernel has been committed.
+cpu_baseline numpy.fft (pocketfft, single thread) on the same kind of complex64 input, forward +
+             inverse, on a bounded sample of the workload, in the same GB/s convention.
+extra        secondary rows of the metric: R2C n = 1024 (C2), pruned rfft2 128^2 m = 16 on
+             [64, 32, 128, 128] (C4) in ms, and rocFFT (torch.fft) on the C1 shape.
+
+Launches rotate over buffer sets totalling well over twice the 256 MB Infinity Cache, so a
+launch cannot read what the previous one left in the cache.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--impl NAME]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "gpu-spectral-stack_amd" / "python"))
+
+N = 1024
+BATCH = 16384
+POINTS = N * BATCH
+BYTES_PER_DIRECTION = 16 * POINTS  # 268,435,456
+PEAK_GBPS = 8000.0
+SETS = 4  # 4 x (x, y, z) x 128 MiB = 1.5 GiB in rotation
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--impl", default="stockham_r8")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="approximate CPU time spent on the numpy baseline sample")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary rows")
+    return ap.parse_args(argv)
+
+
+def load_capi():
+    import torch  # noqa: F401  # PyTorch's HIP runtime first
+
+    import spectral  # noqa: F401  # fails loudly when the extension is not built
+
+    lib = ctypes.CDLL(str(REPO / "gpu-spectral-stack_amd" / "python" / "spectral"
+                          / "libspectral_hip.so"))
+    lib.spx_last_error.restype = ctypes.c_char_p
+    lib.spx_impl_find.argtypes = [ctypes.c_char_p]
+    return lib
+
+
+def traffic_from_profiles(kernel_tag: str):
+    """HBM bytes per launch of the dominant kernel, from a committed rocprof counter summary
+    (profiles/*traffic*.json: {"kernel": ..., "fetch_bytes": ..., "write_bytes": ...}), or None."""
+    for path in sorted((REPO / "profiles").glob("*traffic*.json")):
+        try:
+            data = json.loads(path.read_text())
+        except (OSError, ValueError):
+            continue
+        if data.get("kernel_tag") == kernel_tag:
+            return float(data["fetch_bytes"]) + float(data["write_bytes"])
+    return None
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """numpy.fft forward + inverse over complex64 rows of 1024, timed on this host's cores."""
+    import numpy as np
+
+    rng = np.random.default_rng(1)
+    rows = 2048
+    x = (rng.uniform(-1, 1, (rows, N)) + 1j * rng.uniform(-1, 1, (rows, N))).astype(np.complex64)
+    np.fft.ifft(np.fft.fft(x, axis=-1), axis=-1)  # warm-up
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        np.fft.ifft(np.fft.fft(x, axis=-1), axis=-1)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    gbps = 2 * 16 * rows * N * reps / elapsed / 1e9
+    return {"value": round(gbps, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"numpy {np.__version__} pocketfft fft+ifft complex64, {rows} x {N} rows "
+                      f"repeated {reps}x ({elapsed:.1f} s) on 1 host thread"}
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "batched FFT shards over the batch axis with no exchange, so N GPUs would run N "
+              "independent copies of this workload", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    lib = load_capi()
+    impl = lib.spx_impl_find(args.impl.encode())
+    if impl < 0:
+        raise SystemExit(f"unknown --impl {args.impl}")
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+
+    rng = np.random.default_rng(0)
+    xs, ys, zs = [], [], []
+    for _ in range(SETS):
+        re = torch.from_numpy(rng.uniform(-1, 1, POINTS).astype(np.float32))
+        im = torch.from_numpy(rng.uniform(-1, 1, POINTS).astype(np.float32))
+        xs.append(torch.complex(re, im).to(dev).view(BATCH, N))
+        ys.append(torch.empty(BATCH, N, dtype=torch.complex64, device=dev))
+        zs.append(torch.empty(BATCH, N, dtype=torch.complex64, device=dev))
+    torch.cuda.synchronize()
+
+    def call(src, dst, inverse):
+        rc = lib.spx_c2c(impl, ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()),
+                         N, BATCH, inverse, sptr)
+        if rc != 0:
+            raise RuntimeError(lib.spx_last_error().decode())
+
+    def step(i):
+        s = i % SETS
+        call(xs[s], ys[s], 0)                       # forward of this set
+        call(ys[(s + SETS // 2) % SETS], zs[s], 1)  # inverse of a spectrum written 2 steps ago
+
+    for s in range(SETS):
+        call(xs[s], ys[s], 0)
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # Timed region: exactly K steps between two synchronizations.
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(args.steps):
+        step(i)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    value = 2 * BYTES_PER_DIRECTION / (ms_per_step * 1e6)
+
+    # The dominant kernel alone: forward launches back to back, HIP events on its stream.
+    per_launch = []
+    for _ in range(5):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(20):
+            call(xs[i % SETS], ys[i % SETS], 0)
+        b.record(stream)
+        b.synchronize()
+        per_launch.append(a.elapsed_time(b) / 20)
+    fwd_ms = statistics.median(per_launch)
+    achieved = BYTES_PER_DIRECTION / (fwd_ms * 1e6)
+    kernel_tag = f"c2c_fwd_{args.impl}_n{N}_b{BATCH}"
+    traffic = traffic_from_profiles(kernel_tag)
+
+    extra = {"fwd_ms": round(fwd_ms, 5), "fwd_gbps": round(achieved, 1),
+             "wall_s_timed": round(wall_s, 3)}
+    if not args.no_extra:
+        extra.update(secondary_rows(args.impl, dev))
+
+    line = {
+        "metric": "effective HBM GB/s (% of peak) batched fp32 C2C/R2C at 2^24 points; "
+                  "pruned 2D ms",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "C1: batched C2C forward+inverse, complex64, n=1024, "
+                               "batch=16384 (2^24 points)",
+                   "impl": args.impl, "n": N, "batch": BATCH,
+                   "pct_of_peak": round(100 * value / PEAK_GBPS, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
+                     "traffic": traffic,
+                     "kernel": f"fft_kernel<Plan<1024,8,16>, forward, C2cIo> ({args.impl})",
+                     "bytes_per_launch": BYTES_PER_DIRECTION},
+        "cpu_baseline": cpu_baseline(args.cpu_seconds),
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def secondary_rows(impl: str, dev) -> dict:
+    """R2C n = 1024 (C2), pruned rfft2 on [64, 32, 128, 128] (C4), and rocFFT on the C1 shape."""
+    import torch
+
+    import spectral
+    from spectral.benchmark import fft2_modes_work, fft_real_work, time_gpu
+
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(0)
+    # C2 at n = 1024: 16384 rows, two input sets in rotation.
+    xr = [torch.randn(16384 * 4, 1024, device=dev, generator=g) for _ in range(1)]
+    views = [xr[0][i * 16384:(i + 1) * 16384] for i in range(4)]
+    k = [0]
+
+    def r2c():
+        k[0] += 1
+        return spectral.rfft(views[k[0] % 4], impl=impl)
+
+    t = time_gpu(r2c)
+    out["r2c_1024_ms"] = round(t.median_ms, 5)
+    out["r2c_1024_gbps"] = round(fft_real_work(1024, 16384)[1] / (t.median_ms * 1e6), 1)
+    del xr, views
+    # C4: pruned rfft2, [64, 32, 128, 128] -> modes [64, 32, 32, 16].
+    xp = [torch.randn(64, 32, 128, 128, device=dev, generator=g) for _ in range(3)]
+    k[0] = 0
+
+    def pruned():
+        k[0] += 1
+        return spectral.rfft2_truncated(xp[k[0] % 3], 16, 16, impl=impl)
+
+    t = time_gpu(pruned)
+    out["pruned_rfft2_128_m16_ms"] = round(t.median_ms, 5)
+    out["pruned_rfft2_128_m16_gbps"] = round(
+        fft2_modes_work(128, 128, 16, 16, 2048)[1] / (t.median_ms * 1e6), 1)
+
+    def rocfft_gather():
+        k[0] += 1
+        full = torch.fft.rfft2(xp[k[0] % 3])
+        return torch.cat([full[..., :16, :16], full[..., 112:, :16]], dim=-2)
+
+    t = time_gpu(rocfft_gather)
+    out["rocfft_rfft2_128_plus_gather_ms"] = round(t.median_ms, 5)
+    del xp
+    # rocFFT (through torch.fft) on the C1 shape, forward.
+    xc = [torch.randn(BATCH, N, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
+    k[0] = 0
+
+    def roc():
+        k[0] += 1
+        return torch.fft.fft(xc[k[0] % 3])
+
+    t = time_gpu(roc)
+    out["rocfft_c2c_1024_fwd_ms"] = round(t.median_ms, 5)
+    return out
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,160 @@
+"""Builds the two shared libraries of the MI355X FFT stack, in-tree, for gfx950.
+
+    python gpu-spectral-stack_amd/build.py [--jobs N] [--only capi|torch]
+
+1. libspectral_hip.so: every HIP kernel plus the C ABI of include/spectral_hip.h. Built with
+   hipcc for --offload-arch=gfx950 only; depends on the HIP runtime and nothing from PyTorch.
+2. spectral/_C.so: the PyTorch operators (TORCH_LIBRARY "spectral") over that C ABI. Plain
+   C++ against the PyTorch-ROCm headers, linked to libspectral_hip.so through $ORIGIN.
+
+Both land in python/spectral/, next to the Python package that loads them. Object files go to
+_build/ (git-ignored). Every call recompiles what is older than its sources.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+REPO = ROOT.parent
+CSRC = ROOT / "csrc"
+INCLUDE = REPO / "include"
+PKG = ROOT / "python" / "spectral"
+BUILD = ROOT / "_build"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = str(ROCM / "bin" / "hipcc")
+ARCH = "gfx950"
+
+# Device-code flags. Packed FP32 instructions are switched off: some of their forms have given
+# wrong results on these machines, and the FFT's float arithmetic does not need them.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Wno-unknown-pragmas",
+    "-ffp-contract=fast",
+    "-munsafe-fp-atomics",
+    f"-I{CSRC}",
+    f"-I{INCLUDE}",
+]
+
+CAPI_SOURCES = [
+    "stockham_r2.hip",
+    "stockham_r4.hip",
+    "stockham_r8.hip",
+    "stockham_r8_table.hip",
+    "real.hip",
+    "naive.hip",
+    "scale.hip",
+    "fft2d.hip",
+    "pruned.hip",
+    "registry.cpp",
+    "capi.cpp",
+]
+CAPI_HEADERS = ["spx_common.hpp", "stockham.hpp", "variant.hpp", "fft_api.hpp"]
+
+LIB = PKG / "libspectral_hip.so"
+EXT = PKG / "_C.so"
+
+
+def _stale(target: Path, deps: list[Path]) -> bool:
+    if not target.exists():
+        return True
+    t = target.stat().st_mtime
+    return any(d.stat().st_mtime > t for d in deps)
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise SystemExit(f"build failed: {' '.join(cmd[:3])} ... (exit {proc.returncode})")
+    # The host pass does not know the packed-fp32 target feature; that warning is expected.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    rest = [line for line in (proc.stdout + proc.stderr).splitlines() if noise not in line]
+    if rest:
+        sys.stderr.write("\n".join(rest) + "\n")
+
+
+def _compile(src: Path, force: bool) -> Path:
+    obj = BUILD / (src.name + ".o")
+    deps = [src] + [CSRC / h for h in CAPI_HEADERS] + [INCLUDE / "spectral_hip.h"]
+    if force or _stale(obj, deps):
+        print(f"  hipcc {src.name}", flush=True)
+        lang = [] if src.suffix == ".hip" else ["-x", "hip"]
+        _run([HIPCC, *HIP_FLAGS, *lang, "-c", str(src), "-o", str(obj)])
+    return obj
+
+
+def build_capi(jobs: int, force: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    sources = [CSRC / s for s in CAPI_SOURCES]
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, force), sources))
+    if force or _stale(LIB, objs):
+        print(f"  link {LIB.name}", flush=True)
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(LIB), *map(str, objs),
+              "-Wl,-soname,libspectral_hip.so"])
+    return LIB
+
+
+def _torch_paths() -> tuple[list[str], list[str]]:
+    import torch
+    from torch.utils import cpp_extension
+
+    return cpp_extension.include_paths(), cpp_extension.library_paths()
+
+
+def build_torch(force: bool = False) -> Path:
+    src = CSRC / "torch_ops.cpp"
+    deps = [src, INCLUDE / "spectral_hip.h", LIB]
+    if not (force or _stale(EXT, deps)):
+        return EXT
+    includes, libdirs = _torch_paths()
+    py_include = sysconfig.get_paths()["include"]
+    import torch
+
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    print("  g++ torch_ops.cpp", flush=True)
+    cmd = [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-I{INCLUDE}", f"-I{py_include}", f"-I{ROCM / 'include'}",
+        *[f"-I{p}" for p in includes],
+        str(src), "-o", str(EXT),
+        f"-L{PKG}", "-lspectral_hip",
+        *[f"-L{p}" for p in libdirs],
+        "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lc10_hip", "-ltorch_hip",
+        "-Wl,-rpath,$ORIGIN",
+        *[f"-Wl,-rpath,{p}" for p in libdirs],
+        "-Wno-deprecated-declarations",
+    ]
+    _run(cmd)
+    return EXT
+
+
+def main(argv: list[str] | None = None) -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    ap.add_argument("--only", choices=["capi", "torch"])
+    ap.add_argument("--force", action="store_true", help="recompile everything")
+    args = ap.parse_args(argv)
+    if args.only != "torch":
+        build_capi(args.jobs, args.force)
+    if args.only != "capi":
+        build_torch(args.force)
+
+
+if __name__ == "__main__":
+    main()

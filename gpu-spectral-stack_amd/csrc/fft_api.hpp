@@ -1,0 +1,116 @@
+#pragma once
+
+// The library's internal C++ interface: entry-point contracts, the registry row, and the 2D and
+// pruned drivers. The C ABI (capi.cpp, include/spectral_hip.h) is a thin layer over this.
+//
+// Conventions, as numpy.fft and torch.fft (reference fft.hpp:1-5): batched and out of place,
+// transforms of a batch back to back, forward unnormalized, inverse divided by n.
+
+#include "spx_common.hpp"
+
+#include <cstddef>
+
+namespace spx {
+
+constexpr int kStockhamMaxN = 4096;                          // one kernel, LDS-resident
+constexpr int kFourStepMaxN = kStockhamMaxN * kStockhamMaxN;  // 2^24 (reference fft.hpp:18-21)
+
+// reference fft.hpp:14-15, 36-39, 59-60
+using C2cFn = void (*)(const cf32* x, cf32* y, int n, int batch, Direction direction,
+                       hipStream_t stream);
+using R2cFn = void (*)(const float* x, cf32* y, int n, int batch, cf32* work,
+                       hipStream_t stream);
+using C2rFn = void (*)(const cf32* x, float* y, int n, int batch, cf32* work,
+                       hipStream_t stream);
+using ColumnsFn = void (*)(const cf32* x, cf32* y, int n, int cols, int slabs,
+                           Direction direction, hipStream_t stream);
+
+// reference fft.hpp:62-72
+struct PrunedFns {
+    void (*c2c)(const cf32* x, cf32* y, int n, int batch, int keep, Direction direction,
+                hipStream_t stream);
+    void (*r2c)(const float* x, cf32* y, int n, int batch, int keep, hipStream_t stream);
+    void (*c2r)(const cf32* x, float* y, int n, int batch, int keep, hipStream_t stream);
+    void (*columns)(const cf32* x, cf32* y, int n, int cols, int slabs, int m1_in, int m1_out,
+                    Direction direction, hipStream_t stream);
+};
+
+// One implementation, by name (reference registry.hpp:14-25).
+struct FftImpl {
+    const char* name;
+    C2cFn c2c;
+    R2cFn r2c;
+    C2rFn c2r;
+    ColumnsFn columns;        // strided column transforms, or nullptr (2D then transposes)
+    const PrunedFns* pruned;  // pruning inside the kernels, or nullptr (gather / scatter)
+    int max_n;                // largest complex transform in one kernel (2D, pruned)
+    int max_c2c_n;            // largest 1D complex transform
+    int max_real_n;           // largest real transform
+    bool real_needs_work;     // r2c and c2r use the work buffer
+};
+
+// The registry, in the reference's order (registry.hpp:28-40).
+const FftImpl* impls();
+int impl_count();
+
+// --- naive radix-2 and the generic real path (naive.hip, real.hip) -------------------------
+void c2c_naive(const cf32* x, cf32* y, int n, int batch, Direction direction,
+               hipStream_t stream);
+void r2c_naive(const float* x, cf32* y, int n, int batch, cf32* work, hipStream_t stream);
+void c2r_naive(const cf32* x, float* y, int n, int batch, cf32* work, hipStream_t stream);
+void r2c_via_c2c(C2cFn c2c, const float* x, cf32* y, int n, int batch, cf32* work,
+                 hipStream_t stream);
+void c2r_via_c2c(C2cFn c2c, const cf32* x, float* y, int n, int batch, cf32* work,
+                 hipStream_t stream);
+
+// --- scale (scale.hip) ----------------------------------------------------------------------
+void scale_c2c(const cf32* x, cf32* y, std::size_t n, float alpha, hipStream_t stream);
+
+// --- 2D (fft2d.hip), reference fft2d.hpp:24-39 -----------------------------------------------
+enum class Columns { Transpose, Strided };
+
+std::size_t fft2_c2c_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch);
+std::size_t fft2_r2c_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch);
+std::size_t fft2_c2r_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch);
+void fft2_c2c(const FftImpl& impl, Columns columns, const cf32* x, cf32* y, int n1, int n2,
+              int batch, Direction direction, cf32* work, hipStream_t stream);
+void fft2_r2c(const FftImpl& impl, Columns columns, const float* x, cf32* y, int n1, int n2,
+              int batch, cf32* work, hipStream_t stream);
+void fft2_c2r(const FftImpl& impl, Columns columns, const cf32* x, float* y, int n1, int n2,
+              int batch, cf32* work, hipStream_t stream);
+void transpose(const cf32* x, cf32* y, int rows, int cols, int batch, hipStream_t stream);
+
+// --- pruned (pruned.hip), reference pruned.hpp:26-43 -----------------------------------------
+std::size_t fft_c2c_pruned_workspace(const FftImpl& impl, int n, int keep, int batch);
+std::size_t rfft2_modes_workspace(const FftImpl& impl, int n1, int n2, int m1, int m2, int batch);
+std::size_t irfft2_modes_workspace(const FftImpl& impl, int n1, int n2, int m1, int m2,
+                                   int batch);
+void fft_c2c_pruned(const FftImpl& impl, const cf32* x, cf32* y, int n, int keep, int batch,
+                    Direction direction, cf32* work, hipStream_t stream);
+void rfft2_modes(const FftImpl& impl, const float* x, cf32* modes, int n1, int n2, int m1,
+                 int m2, int batch, cf32* work, hipStream_t stream);
+void irfft2_modes(const FftImpl& impl, const cf32* modes, float* y, int n1, int n2, int m1,
+                  int m2, int batch, cf32* work, hipStream_t stream);
+void gather_modes(const cf32* full, cf32* modes, int n1, int w, int m1, int m2, int batch,
+                  hipStream_t stream);
+void scatter_modes(const cf32* modes, cf32* full, int n1, int w, int m1, int m2, int batch,
+                   hipStream_t stream);
+
+}  // namespace spx
+
+// --- the Stockham variants (stockham_*.hip) ---------------------------------------------------
+#define SPX_DECLARE_VARIANT(NAME)                                                               \
+    void c2c_##NAME(const cf32* x, cf32* y, int n, int batch, Direction direction,             \
+                    hipStream_t stream);                                                        \
+    void r2c_##NAME(const float* x, cf32* y, int n, int batch, cf32* work, hipStream_t stream); \
+    void c2r_##NAME(const cf32* x, float* y, int n, int batch, cf32* work, hipStream_t stream); \
+    void columns_##NAME(const cf32* x, cf32* y, int n, int cols, int slabs,                    \
+                        Direction direction, hipStream_t stream);                               \
+    extern const PrunedFns pruned_##NAME;
+
+namespace spx {
+SPX_DECLARE_VARIANT(stockham_r2)
+SPX_DECLARE_VARIANT(stockham_r4)
+SPX_DECLARE_VARIANT(stockham_r8)
+SPX_DECLARE_VARIANT(stockham_r8_table)
+}  // namespace spx

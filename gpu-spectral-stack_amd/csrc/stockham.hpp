@@ -1,0 +1,722 @@
+#pragma once
+
+// Batched power-of-two FFTs for gfx950: the Stockham autosort recurrence, one workgroup pass per
+// group of transforms, data in registers between stages and LDS only for the exchanges.
+//
+// The recurrence (a textbook algorithm, the same one the reference's stockham.cuh:169-209 runs):
+// a stage of radix R turns sub-transforms of length ns into sub-transforms of length ns * R.
+// Butterfly j (k = j mod ns) takes inputs in[j + r N/R] for r < R, multiplies input r by
+// w^(k r) with w = exp(sign 2 pi i / (ns R)), takes an R-point DFT, and writes output r to
+// out[(j - k) R + k + r ns]. After the last stage the result is in natural order.
+//
+// How this file maps it onto CDNA4 (the design is this repository's own):
+//
+// * Elements per lane E is a separate parameter from the radix. A transform of N points is
+//   owned by L = N / E lanes; each lane holds E values in VGPRs and runs E / R butterflies per
+//   stage (j = lane + b L). The radix only sets the stage count: radix 8 at N = 1024 is
+//   8 x 8 x 8 x 2 with two butterflies per lane per stage.
+// * A workgroup is 256 lanes (four wave64s) and holds T = 256 / L transforms. When L <= 64 every
+//   transform lives inside one wavefront, so the LDS exchanges between stages need only a
+//   wavefront-scope fence (no s_barrier): the four waves of a workgroup never wait for each other.
+// * Contiguous rows (L >= 16) skip LDS on the way in and out: the first stage's inputs
+//   in[j + r N/R] are read straight from HBM (for fixed b, r the lanes of a transform read
+//   consecutive values, runs of L * 8 >= 128 bytes), and the last stage's outputs
+//   out[j + r N/R] are written straight back. Only the stage exchanges touch LDS.
+// * Other access patterns (small N, strided columns, the real-FFT combine that pairs k with
+//   N - k) stage through LDS: the group loads cooperatively and coalesced, then the first stage
+//   reads LDS.
+// * LDS rows are padded by one complex value per 16 (index i is stored at i + i / 16), and the
+//   per-transform stride is odd, so stride-R stage writes and column-major staging spread over
+//   the banks.
+// * Twiddles: one accurate sincospif per butterfly for w^k, then w^(k r) by binary powering
+//   (at most four complex products deep, a few ulp), or a table built once in double precision.
+
+#include "spx_common.hpp"
+
+namespace spx::dev {
+
+constexpr int kBlock = 256;  // lanes per workgroup, every kernel in this file
+
+__host__ __device__ constexpr int clog2(int n)
+{
+    int r = 0;
+    while ((1 << r) < n) {
+        ++r;
+    }
+    return r;
+}
+
+__host__ __device__ constexpr int cmin(int a, int b) { return a < b ? a : b; }
+__host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+// LDS position of element i of a transform: one complex of padding after every 16.
+__host__ __device__ constexpr int pad(int i) { return i + (i >> 4); }
+
+// --- complex arithmetic ---------------------------------------------------------------------
+
+__device__ __forceinline__ cf32 cadd(cf32 a, cf32 b) { return {a.re + b.re, a.im + b.im}; }
+__device__ __forceinline__ cf32 csub(cf32 a, cf32 b) { return {a.re - b.re, a.im - b.im}; }
+__device__ __forceinline__ cf32 cmul(cf32 a, cf32 b)
+{
+    return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
+}
+__device__ __forceinline__ cf32 cscale(cf32 a, float s) { return {a.re * s, a.im * s}; }
+__device__ __forceinline__ cf32 cconj(cf32 a) { return {a.re, -a.im}; }
+__device__ __forceinline__ cf32 czero() { return {0.0f, 0.0f}; }
+
+// a * (sign i), sign = -1 forward, +1 inverse: a swap and one negation.
+template <bool Inv>
+__device__ __forceinline__ cf32 mul_si(cf32 a)
+{
+    if constexpr (Inv) {
+        return {-a.im, a.re};
+    } else {
+        return {a.im, -a.re};
+    }
+}
+
+// exp(i pi a); sincospif reduces pi * a without rounding pi.
+__device__ __forceinline__ cf32 expi_pi(float a)
+{
+    float s = 0.0f;
+    float c = 0.0f;
+    sincospif(a, &s, &c);
+    return {c, s};
+}
+
+// --- R-point DFTs in registers, X[q] = sum_p v[p] exp(sign 2 pi i p q / R) ---------------------
+
+template <int R, bool Inv>
+struct Dft;
+
+template <bool Inv>
+struct Dft<1, Inv> {
+    __device__ __forceinline__ static void run(cf32*) {}
+};
+
+template <bool Inv>
+struct Dft<2, Inv> {
+    __device__ __forceinline__ static void run(cf32* v)
+    {
+        const cf32 a = v[0];
+        v[0] = cadd(a, v[1]);
+        v[1] = csub(a, v[1]);
+    }
+};
+
+template <bool Inv>
+struct Dft<4, Inv> {
+    __device__ __forceinline__ static void run(cf32* v)
+    {
+        const cf32 s02 = cadd(v[0], v[2]);
+        const cf32 d02 = csub(v[0], v[2]);
+        const cf32 s13 = cadd(v[1], v[3]);
+        const cf32 d13 = mul_si<Inv>(csub(v[1], v[3]));
+        v[0] = cadd(s02, s13);
+        v[2] = csub(s02, s13);
+        v[1] = cadd(d02, d13);
+        v[3] = csub(d02, d13);
+    }
+};
+
+// 8 = 2 x 4: DFT4 of the even and of the odd inputs, then X[q] = E[q] + w8^q O[q] and
+// X[q + 4] = E[q] - w8^q O[q]. w8 = (1 + sign i) / sqrt 2, w8^2 = sign i, w8^3 = sign i w8.
+template <bool Inv>
+struct Dft<8, Inv> {
+    __device__ __forceinline__ static void run(cf32* v)
+    {
+        cf32 e[4] = {v[0], v[2], v[4], v[6]};
+        cf32 o[4] = {v[1], v[3], v[5], v[7]};
+        Dft<4, Inv>::run(e);
+        Dft<4, Inv>::run(o);
+        constexpr float h = 0.707106781186547524f;
+        const cf32 o1 = cscale(cadd(o[1], mul_si<Inv>(o[1])), h);   // w8 o1
+        const cf32 o2 = mul_si<Inv>(o[2]);                          // w8^2 o2
+        const cf32 o3 = cscale(csub(mul_si<Inv>(o[3]), o[3]), h);   // w8^3 o3
+        v[0] = cadd(e[0], o[0]);
+        v[4] = csub(e[0], o[0]);
+        v[1] = cadd(e[1], o1);
+        v[5] = csub(e[1], o1);
+        v[2] = cadd(e[2], o2);
+        v[6] = csub(e[2], o2);
+        v[3] = cadd(e[3], o3);
+        v[7] = csub(e[3], o3);
+    }
+};
+
+// 16 = 4 x 4: DFT4 over p for each residue a (inputs v[a + 4 p]), twiddle by w16^(a c), then
+// DFT4 over a; X[c + 4 d] = sum_a w4^(a d) w16^(a c) A_a[c].
+template <bool Inv>
+struct Dft<16, Inv> {
+    __device__ __forceinline__ static void run(cf32* v)
+    {
+        cf32 a[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                a[r][p] = v[r + 4 * p];
+            }
+            Dft<4, Inv>::run(a[r]);
+        }
+        constexpr float c1 = 0.923879532511286756f;  // cos(pi/8)
+        constexpr float s1 = 0.382683432365089772f;  // sin(pi/8)
+        constexpr float h = 0.707106781186547524f;
+        constexpr float sg = Inv ? 1.0f : -1.0f;
+        // w16^m for m = 1, 2, 3, 4, 6, 9 (a * c with a, c in 1..3).
+        const cf32 w1{c1, sg * s1};
+        const cf32 w2{h, sg * h};
+        const cf32 w3{s1, sg * c1};
+        a[1][1] = cmul(a[1][1], w1);
+        a[1][2] = cmul(a[1][2], w2);
+        a[1][3] = cmul(a[1][3], w3);
+        a[2][1] = cmul(a[2][1], w2);
+        a[2][2] = mul_si<Inv>(a[2][2]);                  // w16^4 = sign i
+        a[2][3] = mul_si<Inv>(cmul(a[2][3], w2));        // w16^6 = sign i w16^2
+        a[3][1] = cmul(a[3][1], w3);
+        a[3][2] = mul_si<Inv>(cmul(a[3][2], w2));        // w16^6
+        a[3][3] = cmul(a[3][3], cf32{-c1, -sg * s1});    // w16^9 = -w16^1
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            cf32 t[4] = {a[0][c], a[1][c], a[2][c], a[3][c]};
+            Dft<4, Inv>::run(t);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                v[c + 4 * d] = t[d];
+            }
+        }
+    }
+};
+
+// --- twiddles -------------------------------------------------------------------------------
+
+// Size of the precomputed table: exp(-2 pi i m / kTableN), m < kTableN, rounded once from double.
+constexpr int kTableN = 4096;
+
+// Multiplies u[r] by w^(k r), r = 1 .. R-1, w = exp(sign 2 pi i / Span).
+template <bool Inv, bool Table>
+struct Twiddle {
+    const cf32* table;  // kTableN entries (only when Table)
+
+    template <int R, int Span>
+    __device__ __forceinline__ void apply(cf32* u, int k) const
+    {
+        if constexpr (Table) {
+            static_assert(kTableN % Span == 0, "the table must cover the span");
+            constexpr int step = kTableN / Span;
+#pragma unroll
+            for (int r = 1; r < R; ++r) {
+                const cf32 w = table[k * r * step];  // k r < Span: no wrap
+                u[r] = cmul(u[r], Inv ? cconj(w) : w);
+            }
+        } else {
+            // 2k / Span is exact; sincospif gives w^k to about an ulp.
+            cf32 w1 = expi_pi(2.0f * static_cast<float>(k) / static_cast<float>(Span));
+            if constexpr (!Inv) {
+                w1 = cconj(w1);
+            }
+            cf32 p[R];
+            p[1] = w1;
+#pragma unroll
+            for (int r = 2; r < R; ++r) {
+                p[r] = (r % 2 == 0) ? cmul(p[r / 2], p[r / 2]) : cmul(p[r - 1], w1);
+            }
+#pragma unroll
+            for (int r = 1; r < R; ++r) {
+                u[r] = cmul(u[r], p[r]);
+            }
+        }
+    }
+};
+
+// --- plans ----------------------------------------------------------------------------------
+
+// N-point transform, stages of radix R (then one stage of the leftover factor), E values per lane.
+template <int N_, int R_, int E_>
+struct Plan {
+    static constexpr int N = N_;
+    static constexpr int R = R_ < N_ ? R_ : N_;
+    static constexpr int E = E_;
+    static constexpr int L = N / E;                         // lanes per transform
+    static constexpr int T = kBlock / L;                    // transforms per workgroup
+    static constexpr int kFull = clog2(N) / clog2(R);       // radix-R stages
+    static constexpr int kFinal = N >> (kFull * clog2(R));  // leftover radix (1: none)
+    static constexpr int kStages = kFull + (kFinal > 1 ? 1 : 0);
+    static constexpr int kStride = (pad(N) + 1) | 1;        // odd: LDS distance between transforms
+    static constexpr bool kWaveLocal = L <= 64;             // each transform inside one wave
+
+    static_assert(N >= 2 && (N & (N - 1)) == 0, "N must be a power of two");
+    static_assert(E <= N && N % E == 0 && L <= kBlock, "bad lane split");
+    static_assert(R <= E && kFinal <= E, "a lane must hold a whole butterfly");
+
+    template <int S>
+    static constexpr int radix() { return S < kFull ? R : kFinal; }
+    template <int S>
+    static constexpr int span_before() { return 1 << (S * clog2(R)); }
+};
+
+// Elements per lane for size N: 16 (a radix-16 butterfly, or two radix-8 ones, per lane),
+// fewer for tiny transforms.
+template <int N>
+constexpr int default_e() { return cmin(N, 16); }
+
+// --- synchronization ------------------------------------------------------------------------
+
+template <bool WaveLocal>
+__device__ __forceinline__ void lds_sync()
+{
+    if constexpr (WaveLocal) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    } else {
+        __syncthreads();
+    }
+}
+
+// --- stage pieces ---------------------------------------------------------------------------
+
+template <class P, int S, bool Inv, bool Table>
+__device__ __forceinline__ void stage_compute(cf32 (&v)[P::E], int lane, Twiddle<Inv, Table> tw)
+{
+    constexpr int R = P::template radix<S>();
+    constexpr int NS = P::template span_before<S>();
+#pragma unroll
+    for (int b = 0; b < P::E / R; ++b) {
+        if constexpr (NS > 1) {
+            const int k = (lane + b * P::L) & (NS - 1);
+            tw.template apply<R, NS * R>(&v[b * R], k);
+        }
+        Dft<R, Inv>::run(&v[b * R]);
+    }
+}
+
+// Stage S's outputs to their Stockham positions in LDS.
+template <class P, int S>
+__device__ __forceinline__ void stage_write(cf32* s, const cf32 (&v)[P::E], int lane)
+{
+    constexpr int R = P::template radix<S>();
+    constexpr int NS = P::template span_before<S>();
+#pragma unroll
+    for (int b = 0; b < P::E / R; ++b) {
+        const int j = lane + b * P::L;
+        const int k = j & (NS - 1);
+        const int base = (j - k) * R + k;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            s[pad(base + r * NS)] = v[b * R + r];
+        }
+    }
+}
+
+// Stage S's inputs from LDS: v[b R + r] = s[j + r N / R].
+template <class P, int S>
+__device__ __forceinline__ void stage_read(const cf32* s, cf32 (&v)[P::E], int lane)
+{
+    constexpr int R = P::template radix<S>();
+#pragma unroll
+    for (int b = 0; b < P::E / R; ++b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            v[b * R + r] = s[pad(lane + b * P::L + r * (P::N / R))];
+        }
+    }
+}
+
+// Index of the value held in v[b R + r] as input of stage S (natural order of the transform).
+template <class P, int S>
+__device__ __forceinline__ constexpr int input_index(int lane, int b, int r)
+{
+    return lane + b * P::L + r * (P::N / P::template radix<S>());
+}
+
+// Runs stages S .. kStages-1. On entry v holds stage S's inputs; on exit the last stage's
+// outputs, output r of butterfly b being element lane + b L + r N / R_last.
+template <class P, int S, bool Inv, bool Table>
+__device__ __forceinline__ void run_stages(cf32 (&v)[P::E], cf32* s, int lane,
+                                           Twiddle<Inv, Table> tw)
+{
+    stage_compute<P, S, Inv, Table>(v, lane, tw);
+    if constexpr (S + 1 < P::kStages) {
+        lds_sync<P::kWaveLocal>();  // every lane has read the previous contents of s
+        stage_write<P, S>(s, v, lane);
+        lds_sync<P::kWaveLocal>();
+        stage_read<P, S + 1>(s, v, lane);
+        run_stages<P, S + 1, Inv, Table>(v, s, lane, tw);
+    }
+}
+
+// Writes the last stage's outputs to LDS in natural order (for a staged store).
+template <class P>
+__device__ __forceinline__ void final_write(cf32* s, const cf32 (&v)[P::E], int lane)
+{
+    constexpr int S = P::kStages - 1;
+    constexpr int R = P::template radix<S>();
+#pragma unroll
+    for (int b = 0; b < P::E / R; ++b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            s[pad(lane + b * P::L + r * (P::N / R))] = v[b * R + r];
+        }
+    }
+}
+
+// --- the kernel -----------------------------------------------------------------------------
+//
+// An I/O policy `Io` supplies, for transform t of the batch:
+//   direct_in<P>() / direct_out<P>()   whether the stage-0 inputs are read from global memory by
+//                                the lanes that use them, and the outputs written by the lanes
+//                                that hold them
+//   in<P>(t, i), out<P>(t, i, value)   those direct accesses (element i of transform t)
+//   load<P, W>(lds, first, count, tid, nthreads)    otherwise: fill lds[u * kStride + pad(i)] for
+//   store<P, W>(lds, first, count, tid, nthreads)   the group's transforms u < count, or write
+//                                them out from there; W: the group is one wavefront
+//   kGroupIsBlock                the staged accesses need the whole workgroup (strided columns)
+//
+// A group is the set of transforms the lanes synchronize over: one wavefront when transforms
+// fit in one (and the policy allows it), otherwise the workgroup. Transforms past the end of the
+// batch still run the stages (on whatever is in registers) but touch no global memory, so every
+// lane reaches every barrier.
+template <class P, bool Inv, bool Table, class Io>
+__global__ void __launch_bounds__(kBlock) fft_kernel(Io io, long long batch, const cf32* table)
+{
+    __shared__ cf32 lds[P::T * P::kStride];
+
+    constexpr bool kWaveGroups = P::kWaveLocal && !Io::kGroupIsBlock;
+    constexpr int kGroupThreads = kWaveGroups ? 64 : kBlock;
+    constexpr int kGroupT = kGroupThreads / P::L;  // transforms per group
+
+    const int tid = threadIdx.x;
+    const int u = tid / P::L;  // transform within the workgroup
+    const int lane = tid % P::L;
+    const long long t = static_cast<long long>(blockIdx.x) * P::T + u;
+    const int group = tid / kGroupThreads;
+    const long long group_first = static_cast<long long>(blockIdx.x) * P::T + group * kGroupT;
+    const long long left = batch - group_first;
+    const int group_count = left >= kGroupT ? kGroupT : (left > 0 ? static_cast<int>(left) : 0);
+    cf32* const group_lds = lds + group * kGroupT * P::kStride;
+    cf32* const s = lds + u * P::kStride;
+    const Twiddle<Inv, Table> tw{table};
+
+    cf32 v[P::E];
+    if constexpr (Io::template direct_in<P>()) {
+        if (t < batch) {
+#pragma unroll
+            for (int b = 0; b < P::E / P::template radix<0>(); ++b) {
+#pragma unroll
+                for (int r = 0; r < P::template radix<0>(); ++r) {
+                    v[b * P::template radix<0>() + r] =
+                        io.template in<P>(t, input_index<P, 0>(lane, b, r));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < P::E; ++e) {
+                v[e] = czero();
+            }
+        }
+    } else {
+        io.template load<P, kWaveGroups>(group_lds, group_first, group_count,
+                                         tid % kGroupThreads, kGroupThreads);
+        lds_sync<kWaveGroups>();
+        stage_read<P, 0>(s, v, lane);
+    }
+
+    run_stages<P, 0, Inv, Table>(v, s, lane, tw);
+
+    if constexpr (Io::template direct_out<P>()) {
+        if (t < batch) {
+            constexpr int RL = P::template radix<P::kStages - 1>();
+#pragma unroll
+            for (int b = 0; b < P::E / RL; ++b) {
+#pragma unroll
+                for (int r = 0; r < RL; ++r) {
+                    io.template out<P>(t, lane + b * P::L + r * (P::N / RL), v[b * RL + r]);
+                }
+            }
+        }
+    } else {
+        lds_sync<kWaveGroups>();
+        final_write<P>(s, v, lane);
+        lds_sync<kWaveGroups>();
+        io.template store<P, kWaveGroups>(group_lds, group_first, group_count,
+                                          tid % kGroupThreads, kGroupThreads);
+    }
+}
+
+// --- I/O policies ---------------------------------------------------------------------------
+
+
+// Contiguous complex rows. Pruned: rows of x hold keep_in values (the rest of each transform is
+// zero), rows of y keep_out values.
+template <bool Pruned>
+struct C2cIo {
+    static constexpr bool kGroupIsBlock = false;
+    const cf32* x;
+    cf32* y;
+    float scale;  // applied on the way out: 1/N for the inverse, else 1
+    int keep_in;
+    int keep_out;
+
+    template <class P>
+    static constexpr bool direct_in() { return P::L >= 16; }
+    template <class P>
+    static constexpr bool direct_out() { return P::L >= 16; }
+
+    template <class P>
+    __device__ __forceinline__ cf32 in(long long t, int i) const
+    {
+        if constexpr (Pruned) {
+            return i < keep_in ? x[t * keep_in + i] : czero();
+        } else {
+            return x[t * P::N + i];
+        }
+    }
+
+    template <class P>
+    __device__ __forceinline__ void out(long long t, int i, cf32 v) const
+    {
+        if constexpr (Pruned) {
+            if (i < keep_out) {
+                y[t * keep_out + i] = cscale(v, scale);
+            }
+        } else {
+            y[t * P::N + i] = cscale(v, scale);
+        }
+    }
+
+    template <class P, bool W>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
+                                         int nthreads) const
+    {
+        const int row = Pruned ? keep_in : P::N;
+        const cf32* src = x + first * row;
+        for (int e = tid; e < count * P::N; e += nthreads) {
+            const int u = e / P::N;
+            const int i = e % P::N;
+            cf32 val = czero();
+            if (!Pruned || i < keep_in) {
+                val = src[u * row + i];
+            }
+            lds[u * P::kStride + pad(i)] = val;
+        }
+    }
+
+    template <class P, bool W>
+    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
+                                          int nthreads) const
+    {
+        const int row = Pruned ? keep_out : P::N;
+        cf32* dst = y + first * row;
+        for (int e = tid; e < count * row; e += nthreads) {
+            const int u = e / row;
+            const int i = e - u * row;
+            dst[e] = cscale(lds[u * P::kStride + pad(i)], scale);
+        }
+    }
+};
+
+// Real input (forward). A row of n = 2m reals is read as m complex values z[j] = x[2j] + i x[2j+1]
+// (the same bytes), an m-point forward transform gives Z, and the store combines pairs:
+//   E = (Z[k] + conj Z[m-k]) / 2,  O = (Z[k] - conj Z[m-k]) / 2i,  w = exp(-pi i k / m),
+//   X[k] = E + w O,  X[m-k] = conj(E - w O),
+// so one twiddle serves bins k and m-k (k = 0 pairs with m, whose Z index wraps to 0). This is the
+// split formula of the reference's real.cuh:7-42, evaluated per pair instead of per bin.
+// keep: values per row of y, m + 1 for the whole half spectrum, fewer when pruned.
+struct R2cIo {
+    static constexpr bool kGroupIsBlock = false;
+    const cf32* z;  // x viewed as complex
+    cf32* y;
+    int keep;
+
+    template <class P>
+    static constexpr bool direct_in() { return P::L >= 16; }
+    template <class P>
+    static constexpr bool direct_out() { return false; }
+
+    template <class P>
+    __device__ __forceinline__ cf32 in(long long t, int i) const { return z[t * P::N + i]; }
+    template <class P>
+    __device__ __forceinline__ void out(long long, int, cf32) const {}
+
+    template <class P, bool W>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
+                                         int nthreads) const
+    {
+        C2cIo<false>{z, nullptr, 1.0f, P::N, P::N}.template load<P, W>(lds, first, count, tid,
+                                                                        nthreads);
+    }
+
+    template <class P, bool W>
+    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
+                                          int nthreads) const
+    {
+        constexpr int m = P::N;
+        constexpr int pairs = m / 2 + 1;  // k = 0 .. m/2
+        for (int e = tid; e < count * pairs; e += nthreads) {
+            const int u = e / pairs;
+            const int k = e - u * pairs;
+            const cf32* s = lds + u * P::kStride;
+            const cf32 zk = s[pad(k & (m - 1))];
+            const cf32 zm = s[pad((m - k) & (m - 1))];
+            const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
+            const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};  // (zk - conj zm)/2i
+            const cf32 w = cconj(expi_pi(static_cast<float>(k) / static_cast<float>(m)));
+            const cf32 wo = cmul(w, od);
+            cf32* row = y + (first + u) * keep;
+            if (k < keep) {
+                row[k] = cadd(ev, wo);
+            }
+            if (k < m - k && m - k < keep) {
+                row[m - k] = cconj(csub(ev, wo));
+            }
+        }
+    }
+};
+
+// Real output (inverse). Rows of x hold X[0 .. keep-1] of the m + 1 half-spectrum values (the
+// rest zero). The load prepares pairs (reference real.cuh:44-61, per pair):
+//   E = (X[k] + conj X[m-k]) / 2,  O = (X[k] - conj X[m-k]) / 2 * exp(pi i k / m),
+//   Z[k] = E + i O,  Z[m-k] = conj(E - i O),
+// with the imaginary parts of X[0] and X[m] dropped; then an m-point inverse transform, scaled
+// by 1/m, is the 2m real outputs read as complex.
+struct C2rIo {
+    static constexpr bool kGroupIsBlock = false;
+    const cf32* x;
+    cf32* z;  // y viewed as complex
+    float scale;  // 1/m
+    int keep;
+
+    template <class P>
+    static constexpr bool direct_in() { return false; }
+    template <class P>
+    static constexpr bool direct_out() { return P::L >= 16; }
+
+    template <class P>
+    __device__ __forceinline__ cf32 in(long long, int) const { return czero(); }
+    template <class P>
+    __device__ __forceinline__ void out(long long t, int i, cf32 v) const
+    {
+        z[t * P::N + i] = cscale(v, scale);
+    }
+
+    template <class P, bool W>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
+                                         int nthreads) const
+    {
+        constexpr int m = P::N;
+        // The half spectrum X[0 .. m] into LDS (zero beyond keep).
+        for (int e = tid; e < count * (m + 1); e += nthreads) {
+            const int u = e / (m + 1);
+            const int k = e - u * (m + 1);
+            const cf32 val = k < keep ? x[(first + u) * keep + k] : czero();
+            lds[u * P::kStride + pad(k)] = val;
+        }
+        lds_sync<W>();
+        // Prepare Z in place, one pair (k, m-k) per step: both read and written by one lane.
+        constexpr int pairs = m / 2 + 1;
+        for (int e = tid; e < count * pairs; e += nthreads) {
+            const int u = e / pairs;
+            const int k = e - u * pairs;
+            cf32* s = lds + u * P::kStride;
+            cf32 xk = s[pad(k)];
+            cf32 xm = s[pad(m - k)];
+            if (k == 0) {
+                xk.im = 0.0f;
+                xm.im = 0.0f;
+            }
+            const cf32 ev{0.5f * (xk.re + xm.re), 0.5f * (xk.im - xm.im)};
+            const cf32 d{0.5f * (xk.re - xm.re), 0.5f * (xk.im + xm.im)};
+            const cf32 od = cmul(d, expi_pi(static_cast<float>(k) / static_cast<float>(m)));
+            const cf32 iod{-od.im, od.re};
+            if (k < m) {
+                s[pad(k)] = cadd(ev, iod);
+            }
+            if (k > 0 && k < m - k) {
+                s[pad(m - k)] = cconj(csub(ev, iod));
+            }
+        }
+    }
+
+    template <class P, bool W>
+    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
+                                          int nthreads) const
+    {
+        C2cIo<false>{nullptr, z, scale, P::N, P::N}.template store<P, W>(lds, first, count, tid,
+                                                                          nthreads);
+    }
+};
+
+// Columns of row-major arrays: slabs arrays of N rows by `cols` columns, back to back; transform
+// c is column c % cols of slab c / cols. The whole workgroup stages its T neighbouring columns
+// together, so each row read or written is a run of T * 8 contiguous bytes, and a lane keeps the
+// same column for its whole staging loop (T divides 256), so the slab/column split is computed
+// once.
+//
+// Pruned (an FNO keeps the lowest frequencies of each column): m1_in > 0 means the arrays of x hold
+// only 2 m1_in rows, frequencies 0 .. m1_in-1 then N-m1_in .. N-1 (the rest zero); m1_out > 0
+// that y keeps only those 2 m1_out rows. Frequency i sits in row i (i < m1) or i - (N - 2 m1).
+// x == y is allowed only unpruned: a workgroup reads all its columns before writing any.
+struct StridedIo {
+    static constexpr bool kGroupIsBlock = true;
+    const cf32* x;
+    cf32* y;
+    int cols;
+    float scale;
+    int m1_in;
+    int m1_out;
+
+    template <class P>
+    static constexpr bool direct_in() { return false; }
+    template <class P>
+    static constexpr bool direct_out() { return false; }
+
+    template <class P>
+    __device__ __forceinline__ cf32 in(long long, int) const { return czero(); }
+    template <class P>
+    __device__ __forceinline__ void out(long long, int, cf32) const {}
+
+    template <class P, bool W>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
+                                         int nthreads) const
+    {
+        const int j = tid % P::T;  // this lane's column within the block
+        if (j >= count) {
+            return;
+        }
+        const long long c = first + j;
+        const long long slab = c / cols;
+        const int col = static_cast<int>(c - slab * cols);
+        const int rows = m1_in > 0 ? 2 * m1_in : P::N;
+        const cf32* base = x + slab * rows * cols + col;
+        for (int i = tid / P::T; i < P::N; i += nthreads / P::T) {
+            int row = i;
+            if (m1_in > 0) {
+                row = i < m1_in ? i : (i >= P::N - m1_in ? i - (P::N - rows) : -1);
+            }
+            lds[j * P::kStride + pad(i)] =
+                row >= 0 ? base[static_cast<long long>(row) * cols] : czero();
+        }
+    }
+
+    template <class P, bool W>
+    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
+                                          int nthreads) const
+    {
+        const int j = tid % P::T;
+        if (j >= count) {
+            return;
+        }
+        const long long c = first + j;
+        const long long slab = c / cols;
+        const int col = static_cast<int>(c - slab * cols);
+        const int rows = m1_out > 0 ? 2 * m1_out : P::N;
+        cf32* base = y + slab * rows * cols + col;
+        for (int row = tid / P::T; row < rows; row += nthreads / P::T) {
+            const int i = (m1_out > 0 && row >= m1_out) ? row + (P::N - rows) : row;
+            base[static_cast<long long>(row) * cols] = cscale(lds[j * P::kStride + pad(i)], scale);
+        }
+    }
+};
+
+}  // namespace spx::dev

@@ -1,0 +1,360 @@
+#pragma once
+
+// Host drivers of one Stockham variant (radix R, computed or table twiddles): argument checks,
+// dispatch on the transform size, launch. Each stockham_*.hip file instantiates this header for
+// one variant so the variants compile in parallel.
+//
+// The checks and their messages follow the reference's drivers (stockham.cuh:489-620,
+// real.cu:160-180, fourstep.cuh:110-131): callers and tests match on them.
+
+#include "fft_api.hpp"
+#include "stockham.hpp"
+
+#include <climits>
+
+namespace spx {
+
+// Validation shared by the variants.
+void check_size(int n, const char* who);
+void check_keep(int keep, int n, const char* who);
+void check_real_arguments(const void* real_side, const void* complex_side, int n, int batch,
+                          int complex_row, int max_n, const char* who);
+// n = 2 real transforms (m = 1): the combine / prepare alone (real.cu).
+void r2c_postprocess(const cf32* z, cf32* y, int m, int batch, int keep, hipStream_t stream);
+void c2r_preprocess(const cf32* x, cf32* z, int m, int batch, int keep, hipStream_t stream);
+// The table of exp(-2 pi i m / kTableN) on the current device, built on first use.
+const cf32* twiddle_table();
+
+namespace dev {
+
+template <class P, bool Inv, bool Table, class Io>
+void launch(const Io& io, long long batch, hipStream_t stream)
+{
+    const long long blocks = (batch + P::T - 1) / P::T;
+    const cf32* table = Table ? twiddle_table() : nullptr;
+    hipLaunchKernelGGL((fft_kernel<P, Inv, Table, Io>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kBlock), 0, stream, io, batch, table);
+    SPX_LAUNCH_CHECK();
+}
+
+template <int R, bool Inv, bool Table, class Io>
+void dispatch(int n, const Io& io, long long batch, hipStream_t stream)
+{
+    switch (n) {
+#define SPX_CASE(N)                                                          \
+    case N:                                                                  \
+        launch<Plan<N, R, default_e<N>()>, Inv, Table>(io, batch, stream);   \
+        break;
+        SPX_CASE(2)
+        SPX_CASE(4)
+        SPX_CASE(8)
+        SPX_CASE(16)
+        SPX_CASE(32)
+        SPX_CASE(64)
+        SPX_CASE(128)
+        SPX_CASE(256)
+        SPX_CASE(512)
+        SPX_CASE(1024)
+        SPX_CASE(2048)
+        SPX_CASE(4096)
+#undef SPX_CASE
+    default:
+        throw InvalidArgument("stockham: unsupported size " + str(n));
+    }
+}
+
+template <int R, bool Table, class Io>
+void dispatch_dir(int n, bool inverse, const Io& io, long long batch, hipStream_t stream)
+{
+    if (inverse) {
+        dispatch<R, true, Table>(n, io, batch, stream);
+    } else {
+        dispatch<R, false, Table>(n, io, batch, stream);
+    }
+}
+
+// Four-step (Bailey) rows: batch * n1 rows of N values; element i of row t is multiplied by
+// exp(sign 2 pi i k1 i / (n1 N)), k1 = t mod n1, before the row transform. k1 * i < 2^24 and
+// 2 / (n1 N) is a power of two, so the angle is exact in float.
+struct TwiddleRowsIo {
+    static constexpr bool kGroupIsBlock = false;
+    const cf32* x;
+    cf32* y;
+    float scale;
+    float sign;
+    int n1;
+    float two_over_n;
+
+    template <class P>
+    static constexpr bool direct_in() { return P::L >= 16; }
+    template <class P>
+    static constexpr bool direct_out() { return P::L >= 16; }
+
+    __device__ __forceinline__ cf32 twiddled(long long t, int i, cf32 v) const
+    {
+        const int k1 = static_cast<int>(t & (n1 - 1));
+        cf32 w = expi_pi(static_cast<float>(k1 * i) * two_over_n);
+        w.im *= sign;
+        return cmul(v, w);
+    }
+
+    template <class P>
+    __device__ __forceinline__ cf32 in(long long t, int i) const
+    {
+        return twiddled(t, i, x[t * P::N + i]);
+    }
+
+    template <class P>
+    __device__ __forceinline__ void out(long long t, int i, cf32 v) const
+    {
+        y[t * P::N + i] = cscale(v, scale);
+    }
+
+    template <class P, bool W>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
+                                         int nthreads) const
+    {
+        for (int e = tid; e < count * P::N; e += nthreads) {
+            const int u = e / P::N;
+            const int i = e % P::N;
+            lds[u * P::kStride + pad(i)] = twiddled(first + u, i, x[(first + u) * P::N + i]);
+        }
+    }
+
+    template <class P, bool W>
+    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
+                                          int nthreads) const
+    {
+        C2cIo<false>{nullptr, y, scale, P::N, P::N}.template store<P, W>(lds, first, count, tid,
+                                                                          nthreads);
+    }
+};
+
+}  // namespace dev
+
+// Stream-ordered scratch memory for one four-step call: allocated on `stream`, freed on it after
+// the kernels queued in between, so no device-wide synchronization is needed.
+class StreamWorkspace {
+public:
+    StreamWorkspace(std::size_t count, hipStream_t stream) : stream_(stream)
+    {
+        SPX_HIP_CHECK(hipMallocAsync(reinterpret_cast<void**>(&ptr_), count * sizeof(cf32),
+                                     stream));
+    }
+    ~StreamWorkspace() { (void)hipFreeAsync(ptr_, stream_); }
+    StreamWorkspace(const StreamWorkspace&) = delete;
+    StreamWorkspace& operator=(const StreamWorkspace&) = delete;
+    cf32* get() const { return ptr_; }
+
+private:
+    cf32* ptr_ = nullptr;
+    hipStream_t stream_;
+};
+
+template <int R, bool Table>
+struct Stockham {
+    // Complex transforms of n <= 4096 points. keep prunes the frequency side: forward writes the
+    // first keep outputs, inverse reads the first keep inputs (the rest zero).
+    static void c2c_single(const cf32* x, cf32* y, int n, int batch, Direction direction,
+                           hipStream_t stream, int keep)
+    {
+        check_size(n, "stockham");
+        if (batch < 1) {
+            throw InvalidArgument("stockham: batch must be at least 1, got " + str(batch));
+        }
+        if (keep < 1 || keep > n) {
+            throw InvalidArgument("stockham: keep must be in [1, " + str(n) + "], got "
+                                  + str(keep));
+        }
+        const bool inverse = direction == Direction::Inverse;
+        const int row_in = inverse ? keep : n;
+        const int row_out = inverse ? n : keep;
+        const auto rows = static_cast<std::size_t>(batch);
+        if (x < y + rows * row_out && y < x + rows * row_in) {
+            throw InvalidArgument("stockham: x and y must not overlap (out-of-place only)");
+        }
+        if (n == 1) {
+            SPX_HIP_CHECK(hipMemcpyAsync(y, x, rows * sizeof(cf32), hipMemcpyDeviceToDevice,
+                                         stream));
+            return;
+        }
+        const float scale = inverse ? 1.0f / static_cast<float>(n) : 1.0f;
+        if (keep == n) {
+            dev::dispatch_dir<R, Table>(n, inverse, dev::C2cIo<false>{x, y, scale, n, n}, batch,
+                                        stream);
+        } else {
+            dev::dispatch_dir<R, Table>(n, inverse,
+                                        dev::C2cIo<true>{x, y, scale, row_in, row_out}, batch,
+                                        stream);
+        }
+    }
+
+    // Any power of two up to kFourStepMaxN: one kernel up to 4096, four steps beyond.
+    static void c2c(const cf32* x, cf32* y, int n, int batch, Direction direction,
+                    hipStream_t stream)
+    {
+        if (n <= kStockhamMaxN) {
+            c2c_single(x, y, n, batch, direction, stream, n);
+            return;
+        }
+        if (!is_pow2(n) || n > kFourStepMaxN) {
+            throw InvalidArgument("fourstep: n must be a power of two up to "
+                                  + str(kFourStepMaxN) + ", got " + str(n));
+        }
+        if (batch < 1) {
+            throw InvalidArgument("fourstep: batch must be at least 1, got " + str(batch));
+        }
+        const std::size_t total = static_cast<std::size_t>(n) * static_cast<std::size_t>(batch);
+        if (x < y + total && y < x + total) {
+            throw InvalidArgument("fourstep: x and y must not overlap (out-of-place only)");
+        }
+        constexpr int n2 = kStockhamMaxN;
+        const int n1 = n / n2;
+        if (static_cast<long long>(batch) * n1 > INT_MAX
+            || static_cast<long long>(batch) * n2 > INT_MAX) {
+            throw InvalidArgument("fourstep: too many transforms");
+        }
+        const bool inverse = direction == Direction::Inverse;
+        StreamWorkspace work(total, stream);
+        // 1. n1-point transforms down the n2 columns of each n1 x n2 matrix (x -> y).
+        columns_impl(x, y, n1, n2, batch, direction, stream, 0, 0);
+        // 2 + 3. Twiddle, then n2-point rows (y -> work).
+        const dev::TwiddleRowsIo rows{y,
+                                      work.get(),
+                                      inverse ? 1.0f / static_cast<float>(n2) : 1.0f,
+                                      inverse ? 1.0f : -1.0f,
+                                      n1,
+                                      2.0f / static_cast<float>(n)};
+        dev::dispatch_dir<R, Table>(n2, inverse, rows, static_cast<long long>(batch) * n1,
+                                    stream);
+        // 4. Row k1, column k2 holds X[k1 + n1 k2]: transpose each matrix (work -> y).
+        transpose(work.get(), y, n1, n2, batch, stream);
+    }
+
+    static void columns_impl(const cf32* x, cf32* y, int n, int cols, int slabs,
+                             Direction direction, hipStream_t stream, int m1_in, int m1_out)
+    {
+        check_size(n, "stockham columns");
+        if (cols < 1 || slabs < 1 || static_cast<long long>(cols) * slabs > INT_MAX) {
+            throw InvalidArgument("stockham columns: need 1 <= cols * slabs <= INT_MAX");
+        }
+        if (m1_in < 0 || m1_out < 0 || 2 * m1_in > n || 2 * m1_out > n) {
+            throw InvalidArgument("stockham columns: need 0 <= 2 m1 <= n = " + str(n));
+        }
+        if ((m1_in > 0 || m1_out > 0) && x == y) {
+            throw InvalidArgument("stockham columns: a pruned transform cannot run in place");
+        }
+        const long long batch = static_cast<long long>(cols) * slabs;
+        if (n == 1) {
+            if (x != y) {
+                SPX_HIP_CHECK(hipMemcpyAsync(y, x, static_cast<std::size_t>(batch) * sizeof(cf32),
+                                             hipMemcpyDeviceToDevice, stream));
+            }
+            return;
+        }
+        const bool inverse = direction == Direction::Inverse;
+        const float scale = inverse ? 1.0f / static_cast<float>(n) : 1.0f;
+        dev::dispatch_dir<R, Table>(n, inverse, dev::StridedIo{x, y, cols, scale, m1_in, m1_out},
+                                    batch, stream);
+    }
+
+    static void columns(const cf32* x, cf32* y, int n, int cols, int slabs, Direction direction,
+                        hipStream_t stream)
+    {
+        columns_impl(x, y, n, cols, slabs, direction, stream, 0, 0);
+    }
+
+    static void r2c_impl(const float* x, cf32* y, int n, int batch, hipStream_t stream, int keep)
+    {
+        check_keep(keep, n, "stockham r2c");
+        check_real_arguments(x, y, n, batch, keep, 2 * kStockhamMaxN, "stockham r2c");
+        const int m = n / 2;
+        const auto* z = reinterpret_cast<const cf32*>(x);
+        if (m == 1) {
+            r2c_postprocess(z, y, 1, batch, keep, stream);
+            return;
+        }
+        dev::dispatch_dir<R, Table>(m, false, dev::R2cIo{z, y, keep}, batch, stream);
+    }
+
+    static void c2r_impl(const cf32* x, float* y, int n, int batch, hipStream_t stream, int keep)
+    {
+        check_keep(keep, n, "stockham c2r");
+        check_real_arguments(y, x, n, batch, keep, 2 * kStockhamMaxN, "stockham c2r");
+        const int m = n / 2;
+        auto* z = reinterpret_cast<cf32*>(y);
+        if (m == 1) {
+            c2r_preprocess(x, z, 1, batch, keep, stream);
+            return;
+        }
+        const float scale = 1.0f / static_cast<float>(m);
+        dev::dispatch_dir<R, Table>(m, true, dev::C2rIo{x, z, scale, keep}, batch, stream);
+    }
+
+    static void r2c(const float* x, cf32* y, int n, int batch, cf32*, hipStream_t stream)
+    {
+        r2c_impl(x, y, n, batch, stream, n / 2 + 1);
+    }
+
+    static void c2r(const cf32* x, float* y, int n, int batch, cf32*, hipStream_t stream)
+    {
+        c2r_impl(x, y, n, batch, stream, n / 2 + 1);
+    }
+
+    static void pruned_c2c(const cf32* x, cf32* y, int n, int batch, int keep,
+                           Direction direction, hipStream_t stream)
+    {
+        c2c_single(x, y, n, batch, direction, stream, keep);
+    }
+
+    static void pruned_r2c(const float* x, cf32* y, int n, int batch, int keep,
+                           hipStream_t stream)
+    {
+        r2c_impl(x, y, n, batch, stream, keep);
+    }
+
+    static void pruned_c2r(const cf32* x, float* y, int n, int batch, int keep,
+                           hipStream_t stream)
+    {
+        c2r_impl(x, y, n, batch, stream, keep);
+    }
+
+    static void pruned_columns(const cf32* x, cf32* y, int n, int cols, int slabs, int m1_in,
+                               int m1_out, Direction direction, hipStream_t stream)
+    {
+        columns_impl(x, y, n, cols, slabs, direction, stream, m1_in, m1_out);
+    }
+
+    // Not constexpr on purpose: a constant-initialized table of host function addresses would
+    // also be emitted for the device, where those functions do not exist.
+    static PrunedFns pruned_fns()
+    {
+        return {&pruned_c2c, &pruned_r2c, &pruned_c2r, &pruned_columns};
+    }
+};
+
+}  // namespace spx
+
+// Defines the registry entry points of one variant (declared by SPX_DECLARE_VARIANT).
+#define SPX_DEFINE_VARIANT(NAME, R, TABLE)                                                     \
+    namespace spx {                                                                             \
+    void c2c_##NAME(const cf32* x, cf32* y, int n, int batch, Direction direction,             \
+                    hipStream_t stream)                                                         \
+    {                                                                                           \
+        Stockham<R, TABLE>::c2c(x, y, n, batch, direction, stream);                             \
+    }                                                                                           \
+    void r2c_##NAME(const float* x, cf32* y, int n, int batch, cf32* work, hipStream_t stream) \
+    {                                                                                           \
+        Stockham<R, TABLE>::r2c(x, y, n, batch, work, stream);                                  \
+    }                                                                                           \
+    void c2r_##NAME(const cf32* x, float* y, int n, int batch, cf32* work, hipStream_t stream) \
+    {                                                                                           \
+        Stockham<R, TABLE>::c2r(x, y, n, batch, work, stream);                                  \
+    }                                                                                           \
+    void columns_##NAME(const cf32* x, cf32* y, int n, int cols, int slabs,                    \
+                        Direction direction, hipStream_t stream)                                \
+    {                                                                                           \
+        Stockham<R, TABLE>::columns(x, y, n, cols, slabs, direction, stream);                   \
+    }                                                                                           \
+    const PrunedFns pruned_##NAME = Stockham<R, TABLE>::pruned_fns();                           \
+    }

@@ -1,0 +1,171 @@
+"""NumPy model of the schedule the HIP kernels run, to pin their index logic on the CPU.
+
+Each function mirrors one piece of gpu-spectral-stack_amd/csrc/stockham.hpp (and of the
+reference function it replaces, cited per function) using the same integer formulas, evaluated
+in float64 so that any index mistake shows up as an O(1) error against numpy.fft and the O(N^2)
+definition, never as rounding.
+
+TEST INFRASTRUCTURE: see oracle/__init__.py for who may import this.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+# --- plans (stockham.hpp: Plan, default_e) -----------------------------------------------------
+
+BLOCK = 256  # lanes per workgroup
+
+
+def ilog2(n: int) -> int:
+    return max(0, math.ceil(math.log2(n))) if n > 1 else 0
+
+
+def default_e(n: int) -> int:
+    return min(n, 16)
+
+
+def plan(n: int, radix: int, e: int | None = None) -> dict:
+    """The stage radices and the lane split of an n-point transform with radix-`radix` stages."""
+    e = default_e(n) if e is None else e
+    r = min(radix, n)
+    full = ilog2(n) // ilog2(r)
+    final = n >> (full * ilog2(r))
+    radices = [r] * full + ([final] if final > 1 else [])
+    lanes = n // e
+    assert all(rad <= e for rad in radices), "a lane must hold a whole butterfly"
+    spans = [int(np.prod(radices[:s])) for s in range(len(radices))]  # span before each stage
+    return {"n": n, "e": e, "lanes": lanes, "transforms": BLOCK // lanes, "radices": radices,
+            "spans": spans}
+
+
+def pad(i):
+    """LDS position of element i: one complex of padding after every 16 (stockham.hpp: pad)."""
+    return i + (i >> 4)
+
+
+def stride(n: int) -> int:
+    """LDS distance between transforms (Plan::kStride): holds index n, and odd."""
+    return (pad(n) + 1) | 1
+
+
+# --- the Stockham recurrence (stockham.hpp: stage_compute / stage_write / stage_read) ----------
+# Reference: stockham.cuh:169-209 (the same textbook recurrence).
+
+
+def _dft_matrix(r: int, inverse: bool) -> np.ndarray:
+    sign = 1.0 if inverse else -1.0
+    p = np.arange(r)
+    return np.exp(sign * 2j * np.pi * np.outer(p, p) / r)
+
+
+def stockham(x: np.ndarray, radix: int, inverse: bool = False, e: int | None = None) -> np.ndarray:
+    """Transforms the last axis of x by the kernel's schedule: for every lane and butterfly
+    b < E/R, j = lane + b L, k = j mod ns, inputs in[j + r N/R] times w^(k r), an R-point DFT,
+    outputs to out[(j - k) R + k + r ns]. Unscaled (the kernels scale on the store)."""
+    x = np.asarray(x, dtype=np.complex128)
+    n = x.shape[-1]
+    if n == 1:
+        return x.copy()
+    p = plan(n, radix, e)
+    sign = 1.0 if inverse else -1.0
+    cur = x.copy()
+    for rad, ns in zip(p["radices"], p["spans"]):
+        nxt = np.empty_like(cur)
+        dmat = _dft_matrix(rad, inverse)
+        for lane in range(p["lanes"]):
+            for b in range(p["e"] // rad):
+                j = lane + b * p["lanes"]
+                k = j % ns
+                idx_in = j + np.arange(rad) * (n // rad)
+                w = np.exp(sign * 2j * np.pi * k * np.arange(rad) / (ns * rad))
+                v = cur[..., idx_in] * w
+                out = v @ dmat.T  # X[q] = sum_p v[p] w_R^{pq}
+                idx_out = (j - k) * rad + k + np.arange(rad) * ns
+                nxt[..., idx_out] = out
+        cur = nxt
+    return cur
+
+
+def direct_output_index(n: int, radix: int, lane: int, b: int, r: int, e: int | None = None) -> int:
+    """Element held in v[b R + r] after the last stage (the direct store's index)."""
+    p = plan(n, radix, e)
+    rl = p["radices"][-1]
+    return lane + b * p["lanes"] + r * (n // rl)
+
+
+# --- real transforms by pairs (stockham.hpp: R2cIo::store, C2rIo::load) ------------------------
+# Reference: real.cuh:7-61 (the split formulas; here evaluated once per conjugate pair).
+
+
+def r2c_from_half(z_spec: np.ndarray, keep: int | None = None) -> np.ndarray:
+    """X[0 .. keep-1] of the 2m-point real transform from Z = DFT_m(x viewed as complex), one
+    twiddle per pair (k, m-k): X[k] = E + w O, X[m-k] = conj(E - w O)."""
+    z_spec = np.asarray(z_spec, dtype=np.complex128)
+    m = z_spec.shape[-1]
+    keep = m + 1 if keep is None else keep
+    out = np.zeros(z_spec.shape[:-1] + (keep,), dtype=np.complex128)
+    for k in range(m // 2 + 1):
+        zk = z_spec[..., k % m]
+        zm = z_spec[..., (m - k) % m]
+        ev = 0.5 * (zk + np.conj(zm))
+        od = (zk - np.conj(zm)) / 2j
+        wo = np.exp(-1j * np.pi * k / m) * od
+        if k < keep:
+            out[..., k] = ev + wo
+        if k < m - k and m - k < keep:
+            out[..., m - k] = np.conj(ev - wo)
+    return out
+
+
+def c2r_to_half(x_spec: np.ndarray, m: int) -> np.ndarray:
+    """Z[0 .. m-1] whose m-point inverse DFT, read as 2m reals, is irfft(X, 2m) (before the 1/m
+    scale): Z[k] = E + i O, Z[m-k] = conj(E - i O); Im X[0], Im X[m] dropped. Rows of x_spec hold
+    keep <= m + 1 values, the rest zero."""
+    x_spec = np.asarray(x_spec, dtype=np.complex128)
+    keep = x_spec.shape[-1]
+    full = np.zeros(x_spec.shape[:-1] + (m + 1,), dtype=np.complex128)
+    full[..., :keep] = x_spec[..., : m + 1]
+    z = np.zeros(x_spec.shape[:-1] + (m,), dtype=np.complex128)
+    for k in range(m // 2 + 1):
+        xk = full[..., k].copy()
+        xm = full[..., m - k].copy()
+        if k == 0:
+            xk = xk.real + 0j
+            xm = xm.real + 0j
+        ev = 0.5 * (xk + np.conj(xm))
+        od = 0.5 * (xk - np.conj(xm)) * np.exp(1j * np.pi * k / m)
+        if k < m:
+            z[..., k] = ev + 1j * od
+        if 0 < k < m - k:
+            z[..., m - k] = np.conj(ev - 1j * od)
+    return z
+
+
+# --- index maps of the pruned layouts ----------------------------------------------------------
+
+
+def strided_row(i: int, n: int, m1: int) -> int:
+    """Row of a pruned column array holding frequency i, or -1 (stockham.hpp: StridedIo::load;
+    reference stockham.cuh:380-393)."""
+    if m1 == 0:
+        return i
+    rows = 2 * m1
+    if i < m1:
+        return i
+    if i >= n - m1:
+        return i - (n - rows)
+    return -1
+
+
+def full_index(e: int, n1: int, w: int, m1: int, m2: int) -> int:
+    """Position in the full (arrays of n1 x w) half spectrum of mode e of the (arrays of
+    rows x m2) mode tensor (pruned.hip: full_index; reference pruned.cu:27-39)."""
+    rows = 2 * m1 if m1 > 0 else n1
+    per_array = rows * m2
+    b, rem = divmod(e, per_array)
+    r, c = divmod(rem, m2)
+    row = r + (n1 - rows) if (m1 > 0 and r >= m1) else r
+    return (b * n1 + row) * w + c

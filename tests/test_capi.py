@@ -1,0 +1,141 @@
+"""The C ABI of libspectral_hip.so (include/spectral_hip.h): the library loads, exports every
+declared symbol, reports the registry, and rejects bad arguments with SPX_EINVAL and the
+reference's messages before touching the GPU. On a GPU, direct calls match the oracle."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch  # noqa: F401  # the HIP runtime PyTorch ships must be loaded first
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "spectral_hip.h"
+LIB = REPO / "gpu-spectral-stack_amd" / "python" / "spectral" / "libspectral_hip.so"
+SPX_OK, SPX_EINVAL, SPX_ERUNTIME = 0, 1, 2
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(spx_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        pytest.fail(f"{LIB} is not built: run __graft_entry__.build()")
+    so = ctypes.CDLL(str(LIB))
+    so.spx_impl_name.restype = ctypes.c_char_p
+    so.spx_impl_names.restype = ctypes.c_char_p
+    so.spx_last_error.restype = ctypes.c_char_p
+    so.spx_impl_find.argtypes = [ctypes.c_char_p]
+    return so
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    assert len(names) >= 30
+    for required in ["spx_c2c", "spx_r2c", "spx_c2r", "spx_columns", "spx_fft2_r2c",
+                     "spx_rfft2_modes", "spx_irfft2_modes", "spx_last_error"]:
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [name for name in declared_functions() if not hasattr(lib, name)]
+    assert not missing
+
+
+class Info(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("has_columns", ctypes.c_int),
+                ("has_pruned", ctypes.c_int), ("max_n", ctypes.c_int),
+                ("max_c2c_n", ctypes.c_int), ("max_real_n", ctypes.c_int),
+                ("real_needs_work", ctypes.c_int)]
+
+
+def test_registry_rows(lib):
+    names = [lib.spx_impl_name(i).decode() for i in range(lib.spx_impl_count())]
+    assert names == ["naive", "stockham_r2", "stockham_r4", "stockham_r8", "stockham_r8_table"]
+    assert lib.spx_impl_names().decode() == ", ".join(names)
+    assert lib.spx_impl_find(b"stockham_r8") == 3
+    assert lib.spx_impl_find(b"nope") == -1
+    assert lib.spx_impl_name(99) is None
+    info = Info()
+    assert lib.spx_impl_get_info(0, ctypes.byref(info)) == SPX_OK
+    assert (info.name, info.has_columns, info.has_pruned, info.real_needs_work) == (
+        b"naive", 0, 0, 1)
+    assert info.max_n == info.max_c2c_n == info.max_real_n == 1 << 30
+    assert lib.spx_impl_get_info(3, ctypes.byref(info)) == SPX_OK
+    assert (info.has_columns, info.has_pruned, info.max_n, info.max_c2c_n, info.max_real_n,
+            info.real_needs_work) == (1, 1, 4096, 1 << 24, 8192, 0)
+    assert lib.spx_impl_get_info(9, ctypes.byref(info)) == SPX_EINVAL
+
+
+def _last(lib) -> str:
+    return lib.spx_last_error().decode()
+
+
+def test_argument_errors_come_back_as_einval(lib):
+    # Validation runs before anything is queued, so these need no GPU.
+    p = ctypes.c_void_p(0x1000)
+    q = ctypes.c_void_p(0x100000)
+    assert lib.spx_c2c(99, p, q, 8, 1, 0, None) == SPX_EINVAL
+    assert "unknown FFT implementation" in _last(lib)
+    assert lib.spx_c2c(3, p, q, 12, 1, 0, None) == SPX_EINVAL
+    assert "power of two" in _last(lib)
+    assert lib.spx_c2c(3, p, p, 8, 1, 0, None) == SPX_EINVAL
+    assert "must not overlap" in _last(lib)
+    assert lib.spx_r2c(3, p, q, 16384, 1, None, None) == SPX_EINVAL
+    assert "n must be a power of two from 2 to 8192" in _last(lib)
+    assert lib.spx_r2c(0, p, q, 16, 1, None, None) == SPX_EINVAL
+    assert "needs a workspace" in _last(lib)
+    assert lib.spx_fft2_c2c(3, 1, p, q, 8192, 2, 1, 0, None, None) == SPX_EINVAL
+    assert "n1 to be a power of two up to 4096" in _last(lib)
+    assert lib.spx_fft2_c2c(0, 1, p, q, 8, 8, 1, 0, None, None) == SPX_EINVAL
+    assert "no strided column kernel" in _last(lib)
+    assert lib.spx_rfft2_modes(3, p, q, 8, 8, 5, 2, 1, None, None) == SPX_EINVAL
+    assert "1 <= m1 <= n1/2" in _last(lib)
+    assert lib.spx_pruned_columns(3, p, p, 8, 4, 1, 2, 0, 0, None) == SPX_EINVAL
+    assert "cannot run in place" in _last(lib)
+    assert lib.spx_pruned_c2c(0, p, q, 8, 1, 4, 0, None) == SPX_EINVAL
+    assert "no pruned kernels" in _last(lib)
+
+
+def test_workspace_queries(lib):
+    count = ctypes.c_size_t()
+    assert lib.spx_fft2_c2c_workspace(3, 1, 8, 8, 2, ctypes.byref(count)) == SPX_OK
+    assert count.value == 0
+    assert lib.spx_fft2_c2c_workspace(3, 0, 8, 8, 2, ctypes.byref(count)) == SPX_OK
+    assert count.value == 2 * 8 * 8 * 2
+    assert lib.spx_fft2_r2c_workspace(0, 0, 8, 8, 2, ctypes.byref(count)) == SPX_OK
+    assert count.value == 2 * 8 * 5 * 2 + 8 * 4 * 2
+    assert lib.spx_rfft2_modes_workspace(3, 128, 128, 16, 16, 4, ctypes.byref(count)) == SPX_OK
+    assert count.value == 128 * 16 * 4
+    assert lib.spx_fft_c2c_pruned_workspace(0, 64, 8, 3, ctypes.byref(count)) == SPX_OK
+    assert count.value == 64 * 3
+
+
+@pytest.mark.gpu
+def test_direct_calls_on_an_explicit_stream(lib, rng):
+    from oracle import reference as ref
+    from oracle.tolerance import assert_transform_close, random_complex, random_real
+
+    x = random_complex(rng, (64, 1024))
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.empty_like(xd)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    rc = lib.spx_c2c(3, ctypes.c_void_p(xd.data_ptr()), ctypes.c_void_p(yd.data_ptr()), 1024, 64,
+                     0, ctypes.c_void_p(stream.cuda_stream))
+    assert rc == SPX_OK, _last(lib)
+    stream.synchronize()
+    assert_transform_close(yd, ref.fft(x), 1024)
+
+    r = random_real(rng, (32, 2048))
+    rd = torch.from_numpy(r).cuda()
+    cd = torch.empty(32, 1025, dtype=torch.complex64, device="cuda")
+    rc = lib.spx_r2c(3, ctypes.c_void_p(rd.data_ptr()), ctypes.c_void_p(cd.data_ptr()), 2048, 32,
+                     None, ctypes.c_void_p(stream.cuda_stream))
+    assert rc == SPX_OK, _last(lib)
+    stream.synchronize()
+    assert_transform_close(cd, ref.rfft(r), 2048)
