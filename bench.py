@@ -8,7 +8,8 @@ called through the C ABI (libspectral_hip.so) on one HIP stream.
 value        effective HBM GB/s of the step: algorithmic bytes (16 B per point per direction,
              reference csrc/common/bench.cpp:93-100) / wall time of the timed steps.
 roofline     the forward C2C kernel alone: the same algorithmic bytes per launch / its average
-             launch time measured with HIP events on the stream it runs on; peak = 8000 GB/s.
+             launch time inside the timed region (the K forward launches are queued back to back
+             between two HIP events on the stream they run on); peak = 8000 GB/s.
              `traffic` (HBM bytes per launch from rocprof FETCH_SIZE + WRITE_SIZE) is filled in
              from profiles/ when a counter summary for this kernel has been committed.
 cpu_baseline numpy.fft (pocketfft, single thread) on the same kind of complex64 input, forward +
@@ -28,7 +29,6 @@ import argparse
 import ctypes
 import json
 import os
-import statistics
 import sys
 import time
 from pathlib import Path
@@ -140,8 +140,8 @@ def main(argv=None) -> int:
 
     def step(i):
         s = i % SETS
-        call(xs[s], ys[s], 0)                       # forward of this set
-        call(ys[(s + SETS // 2) % SETS], zs[s], 1)  # inverse of a spectrum written 2 steps ago
+        call(xs[s], ys[s], 0)
+        call(ys[(s + SETS // 2) % SETS], zs[s], 1)
 
     for s in range(SETS):
         call(xs[s], ys[s], 0)
@@ -149,38 +149,35 @@ def main(argv=None) -> int:
         step(i)
     torch.cuda.synchronize()
 
-    # Timed region: exactly K steps between two synchronizations.
+    # Timed region: exactly K steps between two synchronizations, queued as the K forward
+    # transforms back to back, then the K inverse transforms (inverse i reads a spectrum written
+    # four launches earlier, so never one still in the cache). A HIP event between the two halves,
+    # on the stream the kernels run on, gives the forward kernel's average launch duration from
+    # the same region without events between launches.
     start = torch.cuda.Event(enable_timing=True)
+    mid = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record(stream)
     for i in range(args.steps):
-        step(i)
+        call(xs[i % SETS], ys[i % SETS], 0)
+    mid.record(stream)
+    for i in range(args.steps):
+        call(ys[(args.steps + i) % SETS], zs[i % SETS], 1)
     stop.record(stream)
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
     ms_per_step = start.elapsed_time(stop) / args.steps
     value = 2 * BYTES_PER_DIRECTION / (ms_per_step * 1e6)
-
-    # The dominant kernel alone: forward launches back to back, HIP events on its stream.
-    per_launch = []
-    for _ in range(5):
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for i in range(20):
-            call(xs[i % SETS], ys[i % SETS], 0)
-        b.record(stream)
-        b.synchronize()
-        per_launch.append(a.elapsed_time(b) / 20)
-    fwd_ms = statistics.median(per_launch)
+    fwd_ms = start.elapsed_time(mid) / args.steps
+    inv_ms = mid.elapsed_time(stop) / args.steps
     achieved = BYTES_PER_DIRECTION / (fwd_ms * 1e6)
     kernel_tag = f"c2c_fwd_{args.impl}_n{N}_b{BATCH}"
     traffic = traffic_from_profiles(kernel_tag)
 
-    extra = {"fwd_ms": round(fwd_ms, 5), "fwd_gbps": round(achieved, 1),
-             "wall_s_timed": round(wall_s, 3)}
+    extra = {"fwd_ms": round(fwd_ms, 5), "inv_ms": round(inv_ms, 5),
+             "fwd_gbps": round(achieved, 1), "wall_s_timed": round(wall_s, 3)}
     if not args.no_extra:
         extra.update(secondary_rows(args.impl, dev))
 

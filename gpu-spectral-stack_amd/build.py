@@ -1,11 +1,14 @@
 """Builds the two shared libraries of the MI355X FFT stack, in-tree, for gfx950.
 
-    python gpu-spectral-stack_amd/build.py [--jobs N] [--only capi|torch]
+    python gpu-spectral-stack_amd/build.py [--jobs N] [--only capi|torch|tools] [--force]
 
 1. libspectral_hip.so: every HIP kernel plus the C ABI of include/spectral_hip.h. Built with
    hipcc for --offload-arch=gfx950 only; depends on the HIP runtime and nothing from PyTorch.
 2. spectral/_C.so: the PyTorch operators (TORCH_LIBRARY "spectral") over that C ABI. Plain
    C++ against the PyTorch-ROCm headers, linked to libspectral_hip.so through $ORIGIN.
+3. bin/spectral_peaks: the measured copy-bandwidth and FP32 ceilings (csrc/tools/peaks.hip), and
+   bin/spectral_bench: every implementation of every operation next to rocFFT, as CSV
+   (csrc/tools/spectral_bench.cpp, over the C ABI of libspectral_hip.so).
 
 Both land in python/spectral/, next to the Python package that loads them. Object files go to
 _build/ (git-ignored). Every call recompiles what is older than its sources.
@@ -65,6 +68,14 @@ CAPI_HEADERS = ["spx_common.hpp", "stockham.hpp", "variant.hpp", "fft_api.hpp"]
 
 LIB = PKG / "libspectral_hip.so"
 EXT = PKG / "_C.so"
+BIN = ROOT / "bin"
+# name -> (source, extra compile/link arguments)
+TOOLS = {
+    "spectral_peaks": (CSRC / "tools" / "peaks.hip", []),
+    "spectral_bench": (CSRC / "tools" / "spectral_bench.cpp",
+                       ["-x", "hip", f"-L{PKG}", "-lspectral_hip", "-lhipfft",
+                        "-Wl,-rpath,$ORIGIN/../python/spectral"]),
+}
 
 
 def _stale(target: Path, deps: list[Path]) -> bool:
@@ -144,16 +155,33 @@ def build_torch(force: bool = False) -> Path:
     return EXT
 
 
+def build_tools(force: bool = False) -> list[Path]:
+    BIN.mkdir(exist_ok=True)
+    built = []
+    for name, (src, extra) in TOOLS.items():
+        exe = BIN / name
+        if force or _stale(exe, [src, INCLUDE / "spectral_hip.h", LIB]):
+            print(f"  hipcc {src.name} -> bin/{name}", flush=True)
+            lang = extra[:2] if extra[:1] == ["-x"] else []
+            link = extra[len(lang):]
+            _run([HIPCC, *[f for f in HIP_FLAGS if f != "-fPIC"], *lang, str(src), "-o", str(exe),
+                  *link])
+        built.append(exe)
+    return built
+
+
 def main(argv: list[str] | None = None) -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
-    ap.add_argument("--only", choices=["capi", "torch"])
+    ap.add_argument("--only", choices=["capi", "torch", "tools"])
     ap.add_argument("--force", action="store_true", help="recompile everything")
     args = ap.parse_args(argv)
-    if args.only != "torch":
+    if args.only in (None, "capi"):
         build_capi(args.jobs, args.force)
-    if args.only != "capi":
+    if args.only in (None, "torch"):
         build_torch(args.force)
+    if args.only in (None, "tools"):
+        build_tools(args.force)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,231 @@
+// spectral_peaks: the two ceilings of the roofline on this MI355X, measured, as JSON.
+//
+//   copy_gbps    a streaming copy (dwordx4 loads and stores, bytes read + bytes written) over
+//                buffers far larger than the 256 MB Infinity Cache, with the source rotated over
+//                several buffer pairs so no launch reads what the previous one left in the cache.
+//   fp32_gflops  independent FMA chains, no memory traffic (non-packed VALU FMA: packed FP32 is
+//                switched off in every build of this repository).
+//
+// Same role as the reference's csrc/tools/peaks.cu:4-11 (achievable, not datasheet, peaks). The
+// copy kernel also serves as the calibration kernel of known size for the rocprof FETCH_SIZE /
+// WRITE_SIZE counters: `--copy-only --bytes B --iters K` runs exactly K copies of B bytes.
+//
+//   spectral_peaks [--copy-only] [--bytes B] [--iters K] [--out FILE]
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+
+#define CHECK(expr)                                                                       \
+    do {                                                                                  \
+        const hipError_t e_ = (expr);                                                     \
+        if (e_ != hipSuccess) {                                                           \
+            std::fprintf(stderr, "%s failed: %s (%s:%d)\n", #expr, hipGetErrorString(e_), \
+                         __FILE__, __LINE__);                                             \
+            std::exit(1);                                                                 \
+        }                                                                                 \
+    } while (0)
+
+constexpr int kThreads = 256;
+constexpr int kVec = 4;  // float4 per lane per step, 64 bytes in flight per lane
+
+// Each lane copies kVec float4 per step, lanes of a wave adjacent (1 KiB runs per load).
+__global__ void __launch_bounds__(kThreads)
+    copy_kernel(const float4* __restrict__ in, float4* __restrict__ out, std::size_t n)
+{
+    const std::size_t per_step = static_cast<std::size_t>(gridDim.x) * kThreads * kVec;
+    for (std::size_t base = static_cast<std::size_t>(blockIdx.x) * kThreads * kVec + threadIdx.x;
+         base < n; base += per_step) {
+        float4 v[kVec];
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) {
+            const std::size_t i = base + static_cast<std::size_t>(k) * kThreads;
+            if (i < n) {
+                v[k] = in[i];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) {
+            const std::size_t i = base + static_cast<std::size_t>(k) * kThreads;
+            if (i < n) {
+                out[i] = v[k];
+            }
+        }
+    }
+}
+
+constexpr int kChains = 8;
+constexpr int kUnroll = 16;
+
+// a <- a * b + c in kChains independent chains; 0 < b < 1 keeps the values finite. The store is
+// behind a test the compiler cannot fold, so the arithmetic stays.
+__global__ void __launch_bounds__(kThreads) fma_kernel(float* out, int iters, float b, float c)
+{
+    float a[kChains];
+#pragma unroll
+    for (int k = 0; k < kChains; ++k) {
+        a[k] = static_cast<float>(threadIdx.x + k);
+    }
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int j = 0; j < kUnroll; ++j) {
+#pragma unroll
+            for (int k = 0; k < kChains; ++k) {
+                a[k] = fmaf(a[k], b, c);
+            }
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kChains; ++k) {
+        s += a[k];
+    }
+    if (s == -1.0f) {
+        out[blockIdx.x * kThreads + threadIdx.x] = s;
+    }
+}
+
+float median(std::vector<float> v)
+{
+    std::sort(v.begin(), v.end());
+    return v[v.size() / 2];
+}
+
+}  // namespace
+
+int main(int argc, char** argv)
+{
+    bool copy_only = false;
+    std::size_t bytes = std::size_t(1) << 30;  // per buffer
+    int iters = 20;
+    const char* out_path = nullptr;
+    for (int i = 1; i < argc; ++i) {
+        const std::string a = argv[i];
+        if (a == "--copy-only") {
+            copy_only = true;
+        } else if (a == "--bytes" && i + 1 < argc) {
+            bytes = std::strtoull(argv[++i], nullptr, 10);
+        } else if (a == "--iters" && i + 1 < argc) {
+            iters = std::atoi(argv[++i]);
+        } else if (a == "--out" && i + 1 < argc) {
+            out_path = argv[++i];
+        } else {
+            std::fprintf(stderr, "usage: spectral_peaks [--copy-only] [--bytes B] [--iters K] "
+                                 "[--out FILE]\n");
+            return 2;
+        }
+    }
+    if (bytes < 16 || bytes % 16 != 0 || iters < 1) {
+        std::fprintf(stderr, "spectral_peaks: --bytes must be a positive multiple of 16 and "
+                             "--iters at least 1\n");
+        return 2;
+    }
+
+    hipDeviceProp_t prop;
+    CHECK(hipGetDeviceProperties(&prop, 0));
+    const int cus = prop.multiProcessorCount;
+
+    // Rotate the copy over pairs so the sources total at least 1 GiB beyond the cache.
+    const int pairs = static_cast<int>(std::max<std::size_t>(1, (std::size_t(3) << 30) / bytes));
+    const int npairs = std::min(pairs, 4);
+    std::vector<float4*> src(npairs), dst(npairs);
+    const std::size_t n = bytes / sizeof(float4);
+    for (int p = 0; p < npairs; ++p) {
+        CHECK(hipMalloc(&src[p], bytes));
+        CHECK(hipMalloc(&dst[p], bytes));
+        CHECK(hipMemset(src[p], 0x3c, bytes));
+    }
+    const unsigned copy_blocks = static_cast<unsigned>(
+        std::min<std::size_t>((n + kThreads * kVec - 1) / (kThreads * kVec),
+                              static_cast<std::size_t>(cus) * 32));
+    hipEvent_t e0, e1;
+    CHECK(hipEventCreate(&e0));
+    CHECK(hipEventCreate(&e1));
+
+    if (copy_only) {
+        for (int i = 0; i < iters; ++i) {
+            hipLaunchKernelGGL(copy_kernel, dim3(copy_blocks), dim3(kThreads), 0, 0,
+                               src[i % npairs], dst[i % npairs], n);
+        }
+        CHECK(hipGetLastError());
+        CHECK(hipDeviceSynchronize());
+        std::printf("{\"copy_kernel_launches\": %d, \"bytes_read_per_launch\": %zu, "
+                    "\"bytes_written_per_launch\": %zu}\n", iters, bytes, bytes);
+        return 0;
+    }
+
+    // Copy: 3 warm-ups, then 5 rounds of `iters` launches, median per launch.
+    for (int i = 0; i < 3; ++i) {
+        hipLaunchKernelGGL(copy_kernel, dim3(copy_blocks), dim3(kThreads), 0, 0, src[i % npairs],
+                           dst[i % npairs], n);
+    }
+    std::vector<float> copy_ms;
+    for (int r = 0; r < 5; ++r) {
+        CHECK(hipEventRecord(e0, 0));
+        for (int i = 0; i < iters; ++i) {
+            hipLaunchKernelGGL(copy_kernel, dim3(copy_blocks), dim3(kThreads), 0, 0,
+                               src[i % npairs], dst[i % npairs], n);
+        }
+        CHECK(hipEventRecord(e1, 0));
+        CHECK(hipEventSynchronize(e1));
+        float ms = 0.0f;
+        CHECK(hipEventElapsedTime(&ms, e0, e1));
+        copy_ms.push_back(ms / iters);
+    }
+    CHECK(hipGetLastError());
+    const double copy_gbps = 2.0 * static_cast<double>(bytes) / (median(copy_ms) * 1e6);
+
+    // FMA: enough workgroups for 8 waves per SIMD.
+    float* sink = nullptr;
+    const unsigned fma_blocks = static_cast<unsigned>(cus) * 8;
+    CHECK(hipMalloc(&sink, static_cast<std::size_t>(fma_blocks) * kThreads * sizeof(float)));
+    const int fma_iters = 4096;
+    hipLaunchKernelGGL(fma_kernel, dim3(fma_blocks), dim3(kThreads), 0, 0, sink, fma_iters, 0.5f,
+                       1.0f);
+    std::vector<float> fma_ms;
+    for (int r = 0; r < 5; ++r) {
+        CHECK(hipEventRecord(e0, 0));
+        hipLaunchKernelGGL(fma_kernel, dim3(fma_blocks), dim3(kThreads), 0, 0, sink, fma_iters,
+                           0.5f, 1.0f);
+        CHECK(hipEventRecord(e1, 0));
+        CHECK(hipEventSynchronize(e1));
+        float ms = 0.0f;
+        CHECK(hipEventElapsedTime(&ms, e0, e1));
+        fma_ms.push_back(ms);
+    }
+    CHECK(hipGetLastError());
+    const double flops = 2.0 * kChains * kUnroll * static_cast<double>(fma_iters) * fma_blocks
+                         * kThreads;
+    const double fp32_gflops = flops / (median(fma_ms) * 1e6);
+
+    char json[1024];
+    std::snprintf(json, sizeof json,
+                  "{\"device\": \"%s\", \"arch\": \"%s\", \"cus\": %d, \"copy_bytes_per_buffer\": "
+                  "%zu, \"copy_gbps\": %.1f, \"copy_ms\": %.5f, \"fp32_gflops\": %.1f, "
+                  "\"datasheet_hbm_gbps\": 8000.0, \"datasheet_fp32_gflops\": 157300.0}\n",
+                  prop.name, prop.gcnArchName, cus, bytes, copy_gbps, median(copy_ms),
+                  fp32_gflops);
+    std::fputs(json, stdout);
+    if (out_path != nullptr) {
+        FILE* f = std::fopen(out_path, "w");
+        if (f == nullptr) {
+            std::fprintf(stderr, "spectral_peaks: cannot write %s\n", out_path);
+            return 1;
+        }
+        std::fputs(json, f);
+        std::fclose(f);
+    }
+    for (int p = 0; p < npairs; ++p) {
+        CHECK(hipFree(src[p]));
+        CHECK(hipFree(dst[p]));
+    }
+    CHECK(hipFree(sink));
+    return 0;
+}
