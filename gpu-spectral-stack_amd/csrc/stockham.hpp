@@ -28,10 +28,14 @@
 // * LDS rows are padded by one complex value per 16 (index i is stored at i + i / 16), and the
 //   per-transform stride is odd, so stride-R stage writes and column-major staging spread over
 //   the banks.
-// * Twiddles: one accurate sincospif per butterfly for w^k, then w^(k r) by binary powering
-//   (at most four complex products deep, a few ulp), or a table built once in double precision.
+// * Twiddles: one evaluation per lane per stage (exact integer reduction to a quadrant, then
+//   short Taylor series), its powers by complex products, and compile-time constants for the
+//   lane's other butterflies; or a table built once in double precision. LDS addresses are a
+//   per-lane base plus compile-time offsets.
 
 #include "spx_common.hpp"
+
+#include <type_traits>
 
 namespace spx::dev {
 
@@ -82,6 +86,27 @@ __device__ __forceinline__ cf32 expi_pi(float a)
     float c = 0.0f;
     sincospif(a, &s, &c);
     return {c, s};
+}
+
+// --- streaming global accesses ---------------------------------------------------------------
+//
+// Every HBM byte of a transform is read once and written once. Stores always carry the
+// nontemporal hint (they stream through the caches instead of displacing other lines), and so do
+// the loads of complex-to-complex transforms; the loads of the real transforms are plain, which
+// measured faster for them on MI355X (C2C: +4-6 % of peak with both hints; R2C / C2R: +8-12 %
+// with nontemporal stores, but 5-10 % slower again with nontemporal loads).
+
+using f2v = float __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ cf32 ld_stream(const cf32* p)
+{
+    const f2v v = __builtin_nontemporal_load(reinterpret_cast<const f2v*>(p));
+    return {v.x, v.y};
+}
+
+__device__ __forceinline__ void st_stream(cf32* p, cf32 a)
+{
+    __builtin_nontemporal_store(f2v{a.re, a.im}, reinterpret_cast<f2v*>(p));
 }
 
 // --- R-point DFTs in registers, X[q] = sum_p v[p] exp(sign 2 pi i p q / R) ---------------------
@@ -188,46 +213,106 @@ struct Dft<16, Inv> {
     }
 };
 
+// --- compile-time loops ---------------------------------------------------------------------
+
+// f(integral_constant<int, I>) for I = Begin .. End-1, unrolled at compile time, so values that
+// depend on I (twiddle constants, LDS offsets) are constant expressions.
+template <int Begin, int End, class F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    if constexpr (Begin < End) {
+        f(std::integral_constant<int, Begin>{});
+        static_for<Begin + 1, End>(f);
+    }
+}
+
 // --- twiddles -------------------------------------------------------------------------------
+//
+// exp(sign 2 pi i k / Span) with exact argument reduction in integers: 4k = q Span + rem with
+// |rem| <= Span / 2, so the angle is q quarter turns plus r = (pi / 2) rem / Span, |r| <= pi / 4.
+// sin r and cos r come from their Taylor series (through r^9 and r^10; the first omitted terms
+// are below 2e-9 on |r| <= pi/4, far under float rounding), and the quarter turns are applied
+// exactly by swapping and negating. Multiples of a quarter turn come out exact.
+
+constexpr double kPi = 3.14159265358979323846264338327950288;
+
+// Taylor series of sin and cos in double, for compile-time constants (|x| <= pi / 4).
+__host__ __device__ constexpr double taylor_sin(double x)
+{
+    double term = x;
+    double sum = x;
+    for (int n = 1; n < 16; ++n) {
+        term *= -x * x / static_cast<double>((2 * n) * (2 * n + 1));
+        sum += term;
+    }
+    return sum;
+}
+
+__host__ __device__ constexpr double taylor_cos(double x)
+{
+    double term = 1.0;
+    double sum = 1.0;
+    for (int n = 1; n < 16; ++n) {
+        term *= -x * x / static_cast<double>((2 * n - 1) * (2 * n));
+        sum += term;
+    }
+    return sum;
+}
+
+// exp(sign 2 pi i m / span) rounded once to float, at compile time.
+template <bool Inv>
+__host__ __device__ constexpr cf32 const_twiddle(long long m, long long span)
+{
+    m %= span;
+    const long long m4 = 4 * m;
+    const long long q = (m4 + span / 2) / span;  // nearest quarter turn
+    const double r = kPi / 2.0 * static_cast<double>(m4 - q * span) / static_cast<double>(span);
+    const double c = taylor_cos(r);
+    const double s = taylor_sin(r);
+    double re = (q & 1) ? -s : c;
+    double im = (q & 1) ? c : s;
+    if (q & 2) {
+        re = -re;
+        im = -im;
+    }
+    return cf32{static_cast<float>(re), static_cast<float>(Inv ? im : -im)};
+}
+
+// The same at run time, for integer k >= 0 (k < 2^29) and a compile-time power-of-two Span.
+template <int Span, bool Inv>
+__device__ __forceinline__ cf32 twiddle_of(int k)
+{
+    constexpr int kShift = clog2(Span);
+    constexpr double c = kPi / (2.0 * Span);  // r = rem * c, c split so r is rounded once
+    constexpr float c_hi = static_cast<float>(c);
+    constexpr float c_lo = static_cast<float>(c - static_cast<double>(c_hi));
+    const int k4 = k << 2;
+    const int q = (k4 + Span / 2) >> kShift;
+    const float rem = static_cast<float>(k4 - (q << kShift));
+    const float r = fmaf(rem, c_hi, rem * c_lo);
+    const float r2 = r * r;
+    constexpr float s3 = static_cast<float>(-1.0 / 6.0);
+    constexpr float s5 = static_cast<float>(1.0 / 120.0);
+    constexpr float s7 = static_cast<float>(-1.0 / 5040.0);
+    constexpr float s9 = static_cast<float>(1.0 / 362880.0);
+    constexpr float c2 = -0.5f;
+    constexpr float c4 = static_cast<float>(1.0 / 24.0);
+    constexpr float c6 = static_cast<float>(-1.0 / 720.0);
+    constexpr float c8 = static_cast<float>(1.0 / 40320.0);
+    constexpr float c10 = static_cast<float>(-1.0 / 3628800.0);
+    const float sn = fmaf(r * r2, fmaf(r2, fmaf(r2, fmaf(r2, s9, s7), s5), s3), r);
+    const float cs = fmaf(r2, fmaf(r2, fmaf(r2, fmaf(r2, fmaf(r2, c10, c8), c6), c4), c2), 1.0f);
+    float re = (q & 1) ? -sn : cs;
+    float im = (q & 1) ? cs : sn;
+    if (q & 2) {
+        re = -re;
+        im = -im;
+    }
+    return {re, Inv ? im : -im};
+}
 
 // Size of the precomputed table: exp(-2 pi i m / kTableN), m < kTableN, rounded once from double.
 constexpr int kTableN = 4096;
-
-// Multiplies u[r] by w^(k r), r = 1 .. R-1, w = exp(sign 2 pi i / Span).
-template <bool Inv, bool Table>
-struct Twiddle {
-    const cf32* table;  // kTableN entries (only when Table)
-
-    template <int R, int Span>
-    __device__ __forceinline__ void apply(cf32* u, int k) const
-    {
-        if constexpr (Table) {
-            static_assert(kTableN % Span == 0, "the table must cover the span");
-            constexpr int step = kTableN / Span;
-#pragma unroll
-            for (int r = 1; r < R; ++r) {
-                const cf32 w = table[k * r * step];  // k r < Span: no wrap
-                u[r] = cmul(u[r], Inv ? cconj(w) : w);
-            }
-        } else {
-            // 2k / Span is exact; sincospif gives w^k to about an ulp.
-            cf32 w1 = expi_pi(2.0f * static_cast<float>(k) / static_cast<float>(Span));
-            if constexpr (!Inv) {
-                w1 = cconj(w1);
-            }
-            cf32 p[R];
-            p[1] = w1;
-#pragma unroll
-            for (int r = 2; r < R; ++r) {
-                p[r] = (r % 2 == 0) ? cmul(p[r / 2], p[r / 2]) : cmul(p[r - 1], w1);
-            }
-#pragma unroll
-            for (int r = 1; r < R; ++r) {
-                u[r] = cmul(u[r], p[r]);
-            }
-        }
-    }
-};
 
 // --- plans ----------------------------------------------------------------------------------
 
@@ -275,52 +360,138 @@ __device__ __forceinline__ void lds_sync()
 }
 
 // --- stage pieces ---------------------------------------------------------------------------
+//
+// LDS addresses are a per-lane base plus a compile-time offset: pad(a + c) = pad(a) + pad(c)
+// whenever the low four bits of a and c add without a carry, and for every access pattern below
+// that holds for all lanes (power-of-two strides, lane < L). `splits` checks it exhaustively at
+// compile time for each instantiated plan and stage, so a plan where it failed would not build.
 
+template <class P>
+constexpr bool read_splits(int R)
+{
+    for (int lane = 0; lane < P::L; ++lane) {
+        for (int b = 0; b < P::E / R; ++b) {
+            for (int r = 0; r < R; ++r) {
+                const int off = b * P::L + r * (P::N / R);
+                if (pad(lane + off) != pad(lane) + pad(off)) {
+                    return false;
+                }
+            }
+        }
+    }
+    return true;
+}
+
+template <class P>
+constexpr bool write_splits(int R, int NS)
+{
+    for (int lane = 0; lane < P::L; ++lane) {
+        const int k0 = lane & (NS - 1);
+        const int base = (lane - k0) * R + k0;
+        for (int b = 0; b < P::E / R; ++b) {
+            const int kb = (b * P::L) % NS;
+            for (int r = 0; r < R; ++r) {
+                const int off = (b * P::L - kb) * R + kb + r * NS;
+                const int j = lane + b * P::L;  // the definition: k = j mod NS
+                const int k = j & (NS - 1);
+                if ((j - k) * R + k + r * NS != base + off
+                    || pad(base + off) != pad(base) + pad(off)) {
+                    return false;
+                }
+            }
+        }
+    }
+    return true;
+}
+
+// Stage S: twiddles, then E / R DFTs of radix R. Input r of butterfly b (j = lane + b L,
+// k = j mod NS) is multiplied by w^(k r), w = exp(sign 2 pi i / (NS R)). k = (lane mod NS) +
+// ((b L) mod NS), the second term a compile-time multiple of L, so a lane evaluates one twiddle
+// per stage, w^(lane mod NS), takes its powers, and reaches the other butterflies' twiddles
+// through compile-time constants.
 template <class P, int S, bool Inv, bool Table>
-__device__ __forceinline__ void stage_compute(cf32 (&v)[P::E], int lane, Twiddle<Inv, Table> tw)
+__device__ __forceinline__ void stage_compute(cf32 (&v)[P::E], int lane, const cf32* table)
 {
     constexpr int R = P::template radix<S>();
     constexpr int NS = P::template span_before<S>();
+    constexpr int SP = NS * R;
+    constexpr int B = P::E / R;
+    if constexpr (NS > 1) {
+        const int k0 = lane & (NS - 1);
+        if constexpr (Table) {
+            static_assert(kTableN % SP == 0, "the table must cover the span");
+            constexpr int step = kTableN / SP;
+            static_for<0, B>([&](auto bi) {
+                constexpr int b = decltype(bi)::value;
+                const int k = k0 + (b * P::L) % NS;
+                static_for<1, R>([&](auto ri) {
+                    constexpr int r = decltype(ri)::value;
+                    const cf32 w = table[k * r * step];  // k r < SP: no wrap
+                    v[b * R + r] = cmul(v[b * R + r], Inv ? cconj(w) : w);
+                });
+            });
+        } else {
+            cf32 p[R];  // p[r] = w^(k0 r)
+            p[1] = twiddle_of<SP, Inv>(k0);
 #pragma unroll
-    for (int b = 0; b < P::E / R; ++b) {
-        if constexpr (NS > 1) {
-            const int k = (lane + b * P::L) & (NS - 1);
-            tw.template apply<R, NS * R>(&v[b * R], k);
+            for (int r = 2; r < R; ++r) {
+                p[r] = (r % 2 == 0) ? cmul(p[r / 2], p[r / 2]) : cmul(p[r - 1], p[1]);
+            }
+            static_for<0, B>([&](auto bi) {
+                constexpr int b = decltype(bi)::value;
+                constexpr int kb = (b * P::L) % NS;
+                static_for<1, R>([&](auto ri) {
+                    constexpr int r = decltype(ri)::value;
+                    if constexpr (kb == 0) {
+                        v[b * R + r] = cmul(v[b * R + r], p[r]);
+                    } else {
+                        constexpr cf32 c = const_twiddle<Inv>(static_cast<long long>(kb) * r, SP);
+                        v[b * R + r] = cmul(cmul(v[b * R + r], c), p[r]);
+                    }
+                });
+            });
         }
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
         Dft<R, Inv>::run(&v[b * R]);
     }
 }
 
-// Stage S's outputs to their Stockham positions in LDS.
+// Stage S's outputs to their Stockham positions in LDS: output r of butterfly j goes to
+// (j - k) R + k + r NS.
 template <class P, int S>
 __device__ __forceinline__ void stage_write(cf32* s, const cf32 (&v)[P::E], int lane)
 {
     constexpr int R = P::template radix<S>();
     constexpr int NS = P::template span_before<S>();
-#pragma unroll
-    for (int b = 0; b < P::E / R; ++b) {
-        const int j = lane + b * P::L;
-        const int k = j & (NS - 1);
-        const int base = (j - k) * R + k;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            s[pad(base + r * NS)] = v[b * R + r];
-        }
-    }
+    static_assert(write_splits<P>(R, NS), "LDS offsets do not split for this plan");
+    const int k0 = lane & (NS - 1);
+    cf32* const base = s + pad((lane - k0) * R + k0);
+    static_for<0, P::E / R>([&](auto bi) {
+        constexpr int b = decltype(bi)::value;
+        constexpr int kb = (b * P::L) % NS;
+        static_for<0, R>([&](auto ri) {
+            constexpr int r = decltype(ri)::value;
+            base[pad((b * P::L - kb) * R + kb + r * NS)] = v[b * R + r];
+        });
+    });
 }
 
-// Stage S's inputs from LDS: v[b R + r] = s[j + r N / R].
+// Stage S's inputs from LDS: v[b R + r] = s[j + r N / R], j = lane + b L.
 template <class P, int S>
 __device__ __forceinline__ void stage_read(const cf32* s, cf32 (&v)[P::E], int lane)
 {
     constexpr int R = P::template radix<S>();
-#pragma unroll
-    for (int b = 0; b < P::E / R; ++b) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            v[b * R + r] = s[pad(lane + b * P::L + r * (P::N / R))];
-        }
-    }
+    static_assert(read_splits<P>(R), "LDS offsets do not split for this plan");
+    const cf32* const base = s + pad(lane);
+    static_for<0, P::E / R>([&](auto bi) {
+        constexpr int b = decltype(bi)::value;
+        static_for<0, R>([&](auto ri) {
+            constexpr int r = decltype(ri)::value;
+            v[b * R + r] = base[pad(b * P::L + r * (P::N / R))];
+        });
+    });
 }
 
 // Index of the value held in v[b R + r] as input of stage S (natural order of the transform).
@@ -333,16 +504,15 @@ __device__ __forceinline__ constexpr int input_index(int lane, int b, int r)
 // Runs stages S .. kStages-1. On entry v holds stage S's inputs; on exit the last stage's
 // outputs, output r of butterfly b being element lane + b L + r N / R_last.
 template <class P, int S, bool Inv, bool Table>
-__device__ __forceinline__ void run_stages(cf32 (&v)[P::E], cf32* s, int lane,
-                                           Twiddle<Inv, Table> tw)
+__device__ __forceinline__ void run_stages(cf32 (&v)[P::E], cf32* s, int lane, const cf32* table)
 {
-    stage_compute<P, S, Inv, Table>(v, lane, tw);
+    stage_compute<P, S, Inv, Table>(v, lane, table);
     if constexpr (S + 1 < P::kStages) {
         lds_sync<P::kWaveLocal>();  // every lane has read the previous contents of s
         stage_write<P, S>(s, v, lane);
         lds_sync<P::kWaveLocal>();
         stage_read<P, S + 1>(s, v, lane);
-        run_stages<P, S + 1, Inv, Table>(v, s, lane, tw);
+        run_stages<P, S + 1, Inv, Table>(v, s, lane, table);
     }
 }
 
@@ -350,16 +520,57 @@ __device__ __forceinline__ void run_stages(cf32 (&v)[P::E], cf32* s, int lane,
 template <class P>
 __device__ __forceinline__ void final_write(cf32* s, const cf32 (&v)[P::E], int lane)
 {
-    constexpr int S = P::kStages - 1;
-    constexpr int R = P::template radix<S>();
+    constexpr int R = P::template radix<P::kStages - 1>();
+    static_assert(read_splits<P>(R), "LDS offsets do not split for this plan");
+    cf32* const base = s + pad(lane);
+    static_for<0, P::E / R>([&](auto bi) {
+        constexpr int b = decltype(bi)::value;
+        static_for<0, R>([&](auto ri) {
+            constexpr int r = decltype(ri)::value;
+            base[pad(b * P::L + r * (P::N / R))] = v[b * R + r];
+        });
+    });
+}
+
+// --- groups and staged access ---------------------------------------------------------------
+//
+// A group is the set of lanes that stage their transforms through LDS together: one wavefront
+// when a transform fits in one (and the I/O policy allows it), otherwise the whole workgroup.
+// Full: all kT transforms of the group exist; otherwise the group holds the batch's tail and
+// only its first `count` transforms touch global memory.
+template <int T_, int Threads_, bool Full_>
+struct Group {
+    static constexpr int kT = T_;
+    static constexpr int kThreads = Threads_;
+    static constexpr bool kFull = Full_;
+    static constexpr bool kWave = Threads_ <= 64;
+};
+
+// The staged loop over a group's transforms of Row elements each, row-major: element
+// e = u * Row + i goes to lane e mod kThreads at step e / kThreads, so the lanes of a wavefront
+// take consecutive elements and global accesses coalesce whatever Row is. The step count is a
+// compile-time constant: the loops unroll, and a caller that first gathers every step's loads
+// into registers and only then writes LDS keeps all of a lane's loads in flight together.
+template <class G, int Row>
+struct Staged {
+    static constexpr int kTotal = G::kT * Row;
+    static constexpr int kSteps = (kTotal + G::kThreads - 1) / G::kThreads;
+
+    // f(step, u, i, valid); valid: element exists (inside the group and the batch).
+    template <class F>
+    __device__ __forceinline__ static void each(int count, int tid, F&& f)
+    {
 #pragma unroll
-    for (int b = 0; b < P::E / R; ++b) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            s[pad(lane + b * P::L + r * (P::N / R))] = v[b * R + r];
+        for (int k = 0; k < kSteps; ++k) {
+            const int e = tid + k * G::kThreads;
+            const int u = e / Row;
+            const int i = e - u * Row;
+            const bool valid =
+                (kTotal % G::kThreads == 0 || e < kTotal) && (G::kFull || u < count);
+            f(k, u, i, valid);
         }
     }
-}
+};
 
 // --- the kernel -----------------------------------------------------------------------------
 //
@@ -368,15 +579,13 @@ __device__ __forceinline__ void final_write(cf32* s, const cf32 (&v)[P::E], int 
 //                                the lanes that use them, and the outputs written by the lanes
 //                                that hold them
 //   in<P>(t, i), out<P>(t, i, value)   those direct accesses (element i of transform t)
-//   load<P, W>(lds, first, count, tid, nthreads)    otherwise: fill lds[u * kStride + pad(i)] for
-//   store<P, W>(lds, first, count, tid, nthreads)   the group's transforms u < count, or write
-//                                them out from there; W: the group is one wavefront
+//   load<P, G>(lds, first, count, tid)   otherwise: fill lds[u * kStride + pad(i)] for the
+//   store<P, G>(lds, first, count, tid)  group's transforms u < count, or write them out from
+//                                there; tid is the lane's index within the group
 //   kGroupIsBlock                the staged accesses need the whole workgroup (strided columns)
 //
-// A group is the set of transforms the lanes synchronize over: one wavefront when transforms
-// fit in one (and the policy allows it), otherwise the workgroup. Transforms past the end of the
-// batch still run the stages (on whatever is in registers) but touch no global memory, so every
-// lane reaches every barrier.
+// Transforms past the end of the batch still run the stages (on whatever is in registers) but
+// touch no global memory, so every lane reaches every barrier.
 template <class P, bool Inv, bool Table, class Io>
 __global__ void __launch_bounds__(kBlock) fft_kernel(Io io, long long batch, const cf32* table)
 {
@@ -385,18 +594,20 @@ __global__ void __launch_bounds__(kBlock) fft_kernel(Io io, long long batch, con
     constexpr bool kWaveGroups = P::kWaveLocal && !Io::kGroupIsBlock;
     constexpr int kGroupThreads = kWaveGroups ? 64 : kBlock;
     constexpr int kGroupT = kGroupThreads / P::L;  // transforms per group
+    using Full = Group<kGroupT, kGroupThreads, true>;
+    using Tail = Group<kGroupT, kGroupThreads, false>;
 
     const int tid = threadIdx.x;
     const int u = tid / P::L;  // transform within the workgroup
     const int lane = tid % P::L;
     const long long t = static_cast<long long>(blockIdx.x) * P::T + u;
     const int group = tid / kGroupThreads;
+    const int gtid = tid % kGroupThreads;
     const long long group_first = static_cast<long long>(blockIdx.x) * P::T + group * kGroupT;
     const long long left = batch - group_first;
     const int group_count = left >= kGroupT ? kGroupT : (left > 0 ? static_cast<int>(left) : 0);
     cf32* const group_lds = lds + group * kGroupT * P::kStride;
     cf32* const s = lds + u * P::kStride;
-    const Twiddle<Inv, Table> tw{table};
 
     cf32 v[P::E];
     if constexpr (Io::template direct_in<P>()) {
@@ -416,13 +627,16 @@ __global__ void __launch_bounds__(kBlock) fft_kernel(Io io, long long batch, con
             }
         }
     } else {
-        io.template load<P, kWaveGroups>(group_lds, group_first, group_count,
-                                         tid % kGroupThreads, kGroupThreads);
+        if (group_count == kGroupT) {
+            io.template load<P, Full>(group_lds, group_first, kGroupT, gtid);
+        } else {
+            io.template load<P, Tail>(group_lds, group_first, group_count, gtid);
+        }
         lds_sync<kWaveGroups>();
         stage_read<P, 0>(s, v, lane);
     }
 
-    run_stages<P, 0, Inv, Table>(v, s, lane, tw);
+    run_stages<P, 0, Inv, Table>(v, s, lane, table);
 
     if constexpr (Io::template direct_out<P>()) {
         if (t < batch) {
@@ -439,13 +653,15 @@ __global__ void __launch_bounds__(kBlock) fft_kernel(Io io, long long batch, con
         lds_sync<kWaveGroups>();
         final_write<P>(s, v, lane);
         lds_sync<kWaveGroups>();
-        io.template store<P, kWaveGroups>(group_lds, group_first, group_count,
-                                          tid % kGroupThreads, kGroupThreads);
+        if (group_count == kGroupT) {
+            io.template store<P, Full>(group_lds, group_first, kGroupT, gtid);
+        } else {
+            io.template store<P, Tail>(group_lds, group_first, group_count, gtid);
+        }
     }
 }
 
 // --- I/O policies ---------------------------------------------------------------------------
-
 
 // Contiguous complex rows. Pruned: rows of x hold keep_in values (the rest of each transform is
 // zero), rows of y keep_out values.
@@ -467,9 +683,9 @@ struct C2cIo {
     __device__ __forceinline__ cf32 in(long long t, int i) const
     {
         if constexpr (Pruned) {
-            return i < keep_in ? x[t * keep_in + i] : czero();
+            return i < keep_in ? ld_stream(x + t * keep_in + i) : czero();
         } else {
-            return x[t * P::N + i];
+            return ld_stream(x + t * P::N + i);
         }
     }
 
@@ -478,41 +694,42 @@ struct C2cIo {
     {
         if constexpr (Pruned) {
             if (i < keep_out) {
-                y[t * keep_out + i] = cscale(v, scale);
+                st_stream(y + t * keep_out + i, cscale(v, scale));
             }
         } else {
-            y[t * P::N + i] = cscale(v, scale);
+            st_stream(y + t * P::N + i, cscale(v, scale));
         }
     }
 
-    template <class P, bool W>
-    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
-                                         int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
     {
+        using S = Staged<G, P::N>;
         const int row = Pruned ? keep_in : P::N;
         const cf32* src = x + first * row;
-        for (int e = tid; e < count * P::N; e += nthreads) {
-            const int u = e / P::N;
-            const int i = e % P::N;
-            cf32 val = czero();
-            if (!Pruned || i < keep_in) {
-                val = src[u * row + i];
+        cf32 val[S::kSteps];
+        S::each(count, tid, [&](int k, int u, int i, bool valid) {
+            val[k] = (valid && (!Pruned || i < keep_in)) ? ld_stream(src + u * row + i) : czero();
+        });
+        S::each(count, tid, [&](int k, int u, int i, bool valid) {
+            if (valid) {
+                lds[u * P::kStride + pad(i)] = val[k];
             }
-            lds[u * P::kStride + pad(i)] = val;
-        }
+        });
     }
 
-    template <class P, bool W>
-    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
-                                          int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void store(cf32* lds, long long first, int count,
+                                          int tid) const
     {
+        using S = Staged<G, P::N>;
         const int row = Pruned ? keep_out : P::N;
         cf32* dst = y + first * row;
-        for (int e = tid; e < count * row; e += nthreads) {
-            const int u = e / row;
-            const int i = e - u * row;
-            dst[e] = cscale(lds[u * P::kStride + pad(i)], scale);
-        }
+        S::each(count, tid, [&](int, int u, int i, bool valid) {
+            if (valid && (!Pruned || i < keep_out)) {
+                st_stream(dst + u * row + i, cscale(lds[u * P::kStride + pad(i)], scale));
+            }
+        });
     }
 };
 
@@ -539,38 +756,54 @@ struct R2cIo {
     template <class P>
     __device__ __forceinline__ void out(long long, int, cf32) const {}
 
-    template <class P, bool W>
-    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
-                                         int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
     {
-        C2cIo<false>{z, nullptr, 1.0f, P::N, P::N}.template load<P, W>(lds, first, count, tid,
-                                                                        nthreads);
+        using S = Staged<G, P::N>;
+        const cf32* src = z + first * P::N;
+        cf32 val[S::kSteps];
+        S::each(count, tid, [&](int k, int u, int i, bool valid) {
+            val[k] = valid ? src[u * P::N + i] : czero();
+        });
+        S::each(count, tid, [&](int k, int u, int i, bool valid) {
+            if (valid) {
+                lds[u * P::kStride + pad(i)] = val[k];
+            }
+        });
     }
 
-    template <class P, bool W>
-    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
-                                          int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void store(cf32* lds, long long first, int count, int tid) const
     {
         constexpr int m = P::N;
-        constexpr int pairs = m / 2 + 1;  // k = 0 .. m/2
-        for (int e = tid; e < count * pairs; e += nthreads) {
-            const int u = e / pairs;
-            const int k = e - u * pairs;
-            const cf32* s = lds + u * P::kStride;
+        // 1. Combine in place: pair k reads Z[k] and Z[m-k] and writes X[k] and X[m-k] to the
+        //    same two slots (k = 0 reads slot 0 and writes X[0] there and X[m] into slot m), so
+        //    no lane touches another lane's slots.
+        using S = Staged<G, m / 2 + 1>;
+        S::each(count, tid, [&](int, int u, int k, bool valid) {
+            if (!valid) {
+                return;
+            }
+            cf32* s = lds + u * P::kStride;
             const cf32 zk = s[pad(k & (m - 1))];
             const cf32 zm = s[pad((m - k) & (m - 1))];
             const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
             const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};  // (zk - conj zm)/2i
-            const cf32 w = cconj(expi_pi(static_cast<float>(k) / static_cast<float>(m)));
-            const cf32 wo = cmul(w, od);
-            cf32* row = y + (first + u) * keep;
-            if (k < keep) {
-                row[k] = cadd(ev, wo);
+            const cf32 wo = cmul(twiddle_of<2 * m, false>(k), od);  // exp(-pi i k / m) O
+            s[pad(k)] = cadd(ev, wo);
+            if (k < m - k) {
+                s[pad(m - k)] = cconj(csub(ev, wo));
             }
-            if (k < m - k && m - k < keep) {
-                row[m - k] = cconj(csub(ev, wo));
+        });
+        lds_sync<G::kWave>();
+        // 2. The first `keep` values of each row, stored contiguously.
+        using H = Staged<G, m + 1>;
+        cf32* dst = y + first * keep;
+        H::each(count, tid, [&](int, int u, int i, bool valid) {
+            if (valid && i < keep) {
+                st_stream(dst + u * keep + i, lds[u * P::kStride + pad(i)]);
             }
-        }
+        });
     }
 };
 
@@ -583,7 +816,7 @@ struct R2cIo {
 struct C2rIo {
     static constexpr bool kGroupIsBlock = false;
     const cf32* x;
-    cf32* z;  // y viewed as complex
+    cf32* z;      // y viewed as complex
     float scale;  // 1/m
     int keep;
 
@@ -597,27 +830,32 @@ struct C2rIo {
     template <class P>
     __device__ __forceinline__ void out(long long t, int i, cf32 v) const
     {
-        z[t * P::N + i] = cscale(v, scale);
+        st_stream(z + t * P::N + i, cscale(v, scale));
     }
 
-    template <class P, bool W>
-    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
-                                         int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
     {
         constexpr int m = P::N;
         // The half spectrum X[0 .. m] into LDS (zero beyond keep).
-        for (int e = tid; e < count * (m + 1); e += nthreads) {
-            const int u = e / (m + 1);
-            const int k = e - u * (m + 1);
-            const cf32 val = k < keep ? x[(first + u) * keep + k] : czero();
-            lds[u * P::kStride + pad(k)] = val;
-        }
-        lds_sync<W>();
+        using H = Staged<G, m + 1>;
+        const cf32* src = x + first * keep;
+        cf32 val[H::kSteps];
+        H::each(count, tid, [&](int j, int u, int k, bool valid) {
+            val[j] = (valid && k < keep) ? src[u * keep + k] : czero();
+        });
+        H::each(count, tid, [&](int j, int u, int k, bool valid) {
+            if (valid) {
+                lds[u * P::kStride + pad(k)] = val[j];
+            }
+        });
+        lds_sync<G::kWave>();
         // Prepare Z in place, one pair (k, m-k) per step: both read and written by one lane.
-        constexpr int pairs = m / 2 + 1;
-        for (int e = tid; e < count * pairs; e += nthreads) {
-            const int u = e / pairs;
-            const int k = e - u * pairs;
+        using S = Staged<G, m / 2 + 1>;
+        S::each(count, tid, [&](int, int u, int k, bool valid) {
+            if (!valid) {
+                return;
+            }
             cf32* s = lds + u * P::kStride;
             cf32 xk = s[pad(k)];
             cf32 xm = s[pad(m - k)];
@@ -627,7 +865,7 @@ struct C2rIo {
             }
             const cf32 ev{0.5f * (xk.re + xm.re), 0.5f * (xk.im - xm.im)};
             const cf32 d{0.5f * (xk.re - xm.re), 0.5f * (xk.im + xm.im)};
-            const cf32 od = cmul(d, expi_pi(static_cast<float>(k) / static_cast<float>(m)));
+            const cf32 od = cmul(d, twiddle_of<2 * m, true>(k));  // d exp(pi i k / m)
             const cf32 iod{-od.im, od.re};
             if (k < m) {
                 s[pad(k)] = cadd(ev, iod);
@@ -635,15 +873,14 @@ struct C2rIo {
             if (k > 0 && k < m - k) {
                 s[pad(m - k)] = cconj(csub(ev, iod));
             }
-        }
+        });
     }
 
-    template <class P, bool W>
-    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
-                                          int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void store(cf32* lds, long long first, int count,
+                                          int tid) const
     {
-        C2cIo<false>{nullptr, z, scale, P::N, P::N}.template store<P, W>(lds, first, count, tid,
-                                                                          nthreads);
+        C2cIo<false>{nullptr, z, scale, P::N, P::N}.template store<P, G>(lds, first, count, tid);
     }
 };
 
@@ -676,12 +913,14 @@ struct StridedIo {
     template <class P>
     __device__ __forceinline__ void out(long long, int, cf32) const {}
 
-    template <class P, bool W>
-    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
-                                         int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
     {
+        static_assert(G::kT == P::T, "strided columns stage a whole workgroup");
+        constexpr int kRowsPerStep = G::kThreads / P::T;
+        constexpr int kSteps = P::N / kRowsPerStep;
         const int j = tid % P::T;  // this lane's column within the block
-        if (j >= count) {
+        if (!G::kFull && j >= count) {
             return;
         }
         const long long c = first + j;
@@ -689,22 +928,30 @@ struct StridedIo {
         const int col = static_cast<int>(c - slab * cols);
         const int rows = m1_in > 0 ? 2 * m1_in : P::N;
         const cf32* base = x + slab * rows * cols + col;
-        for (int i = tid / P::T; i < P::N; i += nthreads / P::T) {
+        cf32 val[kSteps];
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            const int i = tid / P::T + k * kRowsPerStep;
             int row = i;
             if (m1_in > 0) {
                 row = i < m1_in ? i : (i >= P::N - m1_in ? i - (P::N - rows) : -1);
             }
-            lds[j * P::kStride + pad(i)] =
-                row >= 0 ? base[static_cast<long long>(row) * cols] : czero();
+            val[k] = row >= 0 ? base[static_cast<long long>(row) * cols] : czero();
+        }
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            lds[j * P::kStride + pad(tid / P::T + k * kRowsPerStep)] = val[k];
         }
     }
 
-    template <class P, bool W>
-    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
-                                          int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void store(cf32* lds, long long first, int count,
+                                          int tid) const
     {
+        constexpr int kRowsPerStep = G::kThreads / P::T;
+        constexpr int kSteps = P::N / kRowsPerStep;
         const int j = tid % P::T;
-        if (j >= count) {
+        if (!G::kFull && j >= count) {
             return;
         }
         const long long c = first + j;
@@ -712,9 +959,14 @@ struct StridedIo {
         const int col = static_cast<int>(c - slab * cols);
         const int rows = m1_out > 0 ? 2 * m1_out : P::N;
         cf32* base = y + slab * rows * cols + col;
-        for (int row = tid / P::T; row < rows; row += nthreads / P::T) {
-            const int i = (m1_out > 0 && row >= m1_out) ? row + (P::N - rows) : row;
-            base[static_cast<long long>(row) * cols] = cscale(lds[j * P::kStride + pad(i)], scale);
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            const int row = tid / P::T + k * kRowsPerStep;
+            if (row < rows) {
+                const int i = (m1_out > 0 && row >= m1_out) ? row + (P::N - rows) : row;
+                base[static_cast<long long>(row) * cols] =
+                    cscale(lds[j * P::kStride + pad(i)], scale);
+            }
         }
     }
 };

@@ -110,23 +110,27 @@ struct TwiddleRowsIo {
         y[t * P::N + i] = cscale(v, scale);
     }
 
-    template <class P, bool W>
-    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid,
-                                         int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
     {
-        for (int e = tid; e < count * P::N; e += nthreads) {
-            const int u = e / P::N;
-            const int i = e % P::N;
-            lds[u * P::kStride + pad(i)] = twiddled(first + u, i, x[(first + u) * P::N + i]);
-        }
+        using S = Staged<G, P::N>;
+        const cf32* src = x + first * P::N;
+        cf32 val[S::kSteps];
+        S::each(count, tid, [&](int k, int u, int i, bool valid) {
+            val[k] = valid ? src[u * P::N + i] : czero();
+        });
+        S::each(count, tid, [&](int k, int u, int i, bool valid) {
+            if (valid) {
+                lds[u * P::kStride + pad(i)] = twiddled(first + u, i, val[k]);
+            }
+        });
     }
 
-    template <class P, bool W>
-    __device__ __forceinline__ void store(const cf32* lds, long long first, int count, int tid,
-                                          int nthreads) const
+    template <class P, class G>
+    __device__ __forceinline__ void store(cf32* lds, long long first, int count,
+                                          int tid) const
     {
-        C2cIo<false>{nullptr, y, scale, P::N, P::N}.template store<P, W>(lds, first, count, tid,
-                                                                          nthreads);
+        C2cIo<false>{nullptr, y, scale, P::N, P::N}.template store<P, G>(lds, first, count, tid);
     }
 };
 
