@@ -202,7 +202,7 @@ def main(argv=None) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
                      "traffic": traffic,
-                     "kernel": f"fft_kernel<Plan<1024,8,16>, forward, C2cIo> ({args.impl})",
+                     "kernel": f"fft_kernel<Plan<1024, R, E>, forward, C2cIo<false>> ({args.impl})",
                      "bytes_per_launch": BYTES_PER_DIRECTION},
         "cpu_baseline": cpu_baseline(args.cpu_seconds),
         "extra": extra,

@@ -9,6 +9,7 @@
 #include "variant.hpp"
 
 #include <algorithm>
+#include <cstdint>
 #include <cmath>
 #include <mutex>
 #include <vector>
@@ -153,7 +154,129 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
+// n = 2 (m = 1), one row per lane: X[0] = x0 + x1 and X[1] = x0 - x1 (both real), from one 8-byte
+// load to one 16-byte store (8 bytes when keep = 1). The grid covers the rows once, so every lane
+// moves exactly one row, the pattern that streams best.
+using f2v = float __attribute__((ext_vector_type(2)));
+using f4v = float __attribute__((ext_vector_type(4)));
+
+template <bool Vec>
+__global__ void __launch_bounds__(kThreads)
+    r2c_n2_kernel(const f2v* __restrict__ x, cf32* __restrict__ y, int keep, std::size_t rows)
+{
+    const std::size_t row = blockIdx.x * static_cast<std::size_t>(kThreads) + threadIdx.x;
+    if (row >= rows) {
+        return;
+    }
+    const f2v v = x[row];
+    const float x0 = v.x + v.y;
+    const float x1 = v.x - v.y;
+    if (keep == 2) {
+        if constexpr (Vec) {
+            __builtin_nontemporal_store(f4v{x0, 0.0f, x1, 0.0f}, reinterpret_cast<f4v*>(y) + row);
+        } else {
+            __builtin_nontemporal_store(f2v{x0, 0.0f}, reinterpret_cast<f2v*>(y + 2 * row));
+            __builtin_nontemporal_store(f2v{x1, 0.0f}, reinterpret_cast<f2v*>(y + 2 * row + 1));
+        }
+    } else {
+        __builtin_nontemporal_store(f2v{x0, 0.0f}, reinterpret_cast<f2v*>(y + row));
+    }
+}
+
+// The inverse for n = 2: y0 = (X[0] + X[1]) / 2, y1 = (X[0] - X[1]) / 2, real parts only (the
+// imaginary parts of the DC and Nyquist bins are ignored; X[1] = 0 when keep = 1).
+template <bool Vec>
+__global__ void __launch_bounds__(kThreads)
+    c2r_n2_kernel(const cf32* __restrict__ x, f2v* __restrict__ y, int keep, std::size_t rows)
+{
+    const std::size_t row = blockIdx.x * static_cast<std::size_t>(kThreads) + threadIdx.x;
+    if (row >= rows) {
+        return;
+    }
+    float a = 0.0f;
+    float b = 0.0f;
+    if (keep == 2) {
+        if constexpr (Vec) {
+            const f4v v = reinterpret_cast<const f4v*>(x)[row];
+            a = v.x;
+            b = v.z;
+        } else {
+            a = x[2 * row].re;
+            b = x[2 * row + 1].re;
+        }
+    } else {
+        a = x[row].re;
+    }
+    __builtin_nontemporal_store(f2v{0.5f * (a + b), 0.5f * (a - b)}, y + row);
+}
+
+// The inverse for n = 4, one row per lane: from X[0], X[1] = p + iq, X[2] (the rest zero beyond
+// keep; imaginary parts of X[0] and X[2] ignored), y[t] = (X0 + 2 Re(X1 i^t) + (-1)^t X2) / 4:
+//   y0 = (a + 2p + c) / 4,  y1 = (a - 2q - c) / 4,  y2 = (a - 2p + c) / 4,  y3 = (a + 2q - c) / 4.
+__global__ void __launch_bounds__(kThreads)
+    c2r_n4_kernel(const cf32* __restrict__ x, f4v* __restrict__ y, int keep, std::size_t rows)
+{
+    const std::size_t row = blockIdx.x * static_cast<std::size_t>(kThreads) + threadIdx.x;
+    if (row >= rows) {
+        return;
+    }
+    const cf32* in = x + row * static_cast<std::size_t>(keep);
+    const float a = in[0].re;
+    const cf32 x1 = keep > 1 ? in[1] : cf32{0.0f, 0.0f};
+    const float c = keep > 2 ? in[2].re : 0.0f;
+    const float ac = a + c;
+    const float amc = a - c;
+    const float p2 = 2.0f * x1.re;
+    const float q2 = 2.0f * x1.im;
+    __builtin_nontemporal_store(
+        f4v{0.25f * (ac + p2), 0.25f * (amc - q2), 0.25f * (ac - p2), 0.25f * (amc + q2)},
+        y + row);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15) == 0; }
+
 }  // namespace
+
+void r2c_n2(const float* x, cf32* y, int batch, int keep, hipStream_t stream)
+{
+    const auto rows = static_cast<std::size_t>(batch);
+    const dim3 grid(static_cast<unsigned>((rows + kThreads - 1) / kThreads));
+    const auto* xv = reinterpret_cast<const f2v*>(x);
+    if (aligned16(y)) {
+        hipLaunchKernelGGL(r2c_n2_kernel<true>, grid, dim3(kThreads), 0, stream, xv, y, keep, rows);
+    } else {
+        hipLaunchKernelGGL(r2c_n2_kernel<false>, grid, dim3(kThreads), 0, stream, xv, y, keep,
+                           rows);
+    }
+    SPX_LAUNCH_CHECK();
+}
+
+void c2r_n2(const cf32* x, float* y, int batch, int keep, hipStream_t stream)
+{
+    const auto rows = static_cast<std::size_t>(batch);
+    const dim3 grid(static_cast<unsigned>((rows + kThreads - 1) / kThreads));
+    auto* yv = reinterpret_cast<f2v*>(y);
+    if (aligned16(x)) {
+        hipLaunchKernelGGL(c2r_n2_kernel<true>, grid, dim3(kThreads), 0, stream, x, yv, keep, rows);
+    } else {
+        hipLaunchKernelGGL(c2r_n2_kernel<false>, grid, dim3(kThreads), 0, stream, x, yv, keep,
+                           rows);
+    }
+    SPX_LAUNCH_CHECK();
+}
+
+bool c2r_n4(const cf32* x, float* y, int batch, int keep, hipStream_t stream)
+{
+    if (!aligned16(y)) {
+        return false;  // the caller runs the general kernel instead
+    }
+    const auto rows = static_cast<std::size_t>(batch);
+    const dim3 grid(static_cast<unsigned>((rows + kThreads - 1) / kThreads));
+    hipLaunchKernelGGL(c2r_n4_kernel, grid, dim3(kThreads), 0, stream, x,
+                       reinterpret_cast<f4v*>(y), keep, rows);
+    SPX_LAUNCH_CHECK();
+    return true;
+}
 
 void r2c_postprocess(const cf32* z, cf32* y, int m, int batch, int keep, hipStream_t stream)
 {

@@ -14,10 +14,11 @@
 // * Elements per lane E is a separate parameter from the radix. A transform of N points is
 //   owned by L = N / E lanes; each lane holds E values in VGPRs and runs E / R butterflies per
 //   stage (j = lane + b L). The radix only sets the stage count: radix 8 at N = 1024 is
-//   8 x 8 x 8 x 2 with two butterflies per lane per stage.
+//   8 x 8 x 8 x 2; with E = 8 a lane runs one radix-8 butterfly per stage, then four radix-2.
 // * A workgroup is 256 lanes (four wave64s) and holds T = 256 / L transforms. When L <= 64 every
 //   transform lives inside one wavefront, so the LDS exchanges between stages need only a
 //   wavefront-scope fence (no s_barrier): the four waves of a workgroup never wait for each other.
+//   E is chosen per (N, R) by default_e: small, for occupancy.
 // * Contiguous rows (L >= 16) skip LDS on the way in and out: the first stage's inputs
 //   in[j + r N/R] are read straight from HBM (for fixed b, r the lanes of a transform read
 //   consecutive values, runs of L * 8 >= 128 bytes), and the last stage's outputs
@@ -29,8 +30,9 @@
 //   per-transform stride is odd, so stride-R stage writes and column-major staging spread over
 //   the banks.
 // * Twiddles: one evaluation per lane per stage (exact integer reduction to a quadrant, then
-//   short Taylor series), its powers by complex products, and compile-time constants for the
-//   lane's other butterflies; or a table built once in double precision. LDS addresses are a
+//   short Taylor series; or, in the table variants, one lookup in a table built once in double
+//   precision), its powers by complex products, and compile-time constants for the lane's other
+//   butterflies. LDS addresses are a
 //   per-lane base plus compile-time offsets.
 
 #include "spx_common.hpp"
@@ -39,7 +41,8 @@
 
 namespace spx::dev {
 
-constexpr int kBlock = 256;  // lanes per workgroup, every kernel in this file
+constexpr int kBlock = 256;      // lanes per workgroup, unless one transform needs more
+constexpr int kMaxBlock = 1024;  // the largest workgroup
 
 __host__ __device__ constexpr int clog2(int n)
 {
@@ -323,7 +326,8 @@ struct Plan {
     static constexpr int R = R_ < N_ ? R_ : N_;
     static constexpr int E = E_;
     static constexpr int L = N / E;                         // lanes per transform
-    static constexpr int T = kBlock / L;                    // transforms per workgroup
+    static constexpr int kThreads = L > kBlock ? L : kBlock;  // lanes per workgroup
+    static constexpr int T = kThreads / L;                    // transforms per workgroup
     static constexpr int kFull = clog2(N) / clog2(R);       // radix-R stages
     static constexpr int kFinal = N >> (kFull * clog2(R));  // leftover radix (1: none)
     static constexpr int kStages = kFull + (kFinal > 1 ? 1 : 0);
@@ -331,7 +335,7 @@ struct Plan {
     static constexpr bool kWaveLocal = L <= 64;             // each transform inside one wave
 
     static_assert(N >= 2 && (N & (N - 1)) == 0, "N must be a power of two");
-    static_assert(E <= N && N % E == 0 && L <= kBlock, "bad lane split");
+    static_assert(E <= N && N % E == 0 && L <= kMaxBlock, "bad lane split");
     static_assert(R <= E && kFinal <= E, "a lane must hold a whole butterfly");
 
     template <int S>
@@ -340,10 +344,16 @@ struct Plan {
     static constexpr int span_before() { return 1 << (S * clog2(R)); }
 };
 
-// Elements per lane for size N: 16 (a radix-16 butterfly, or two radix-8 ones, per lane),
-// fewer for tiny transforms.
-template <int N>
-constexpr int default_e() { return cmin(N, 16); }
+// Values per lane for an N-point transform with radix-R stages: as few as hold one butterfly (and
+// at least 4: radix-2 plans with E = 2 measured 15-20 % slower), but enough that a transform needs
+// at most 256 lanes. Fewer values per lane means fewer VGPRs and more resident waves, and on
+// MI355X that is what raised the sustained bandwidth: at N = 1024 radix 4, E = 4 / 8 / 16 measured
+// 76 / 75 / 72 % of the 8 TB/s peak; larger workgroups (N = 4096 with E = 8 or 4) measured lower.
+template <int N, int R>
+constexpr int default_e()
+{
+    return cmin(N, cmax(cmax(R, 4), N / kBlock));
+}
 
 // --- synchronization ------------------------------------------------------------------------
 
@@ -406,9 +416,9 @@ constexpr bool write_splits(int R, int NS)
 
 // Stage S: twiddles, then E / R DFTs of radix R. Input r of butterfly b (j = lane + b L,
 // k = j mod NS) is multiplied by w^(k r), w = exp(sign 2 pi i / (NS R)). k = (lane mod NS) +
-// ((b L) mod NS), the second term a compile-time multiple of L, so a lane evaluates one twiddle
-// per stage, w^(lane mod NS), takes its powers, and reaches the other butterflies' twiddles
-// through compile-time constants.
+// ((b L) mod NS), the second term a compile-time multiple of L, so a lane evaluates (or looks up)
+// one twiddle per stage, w^(lane mod NS), takes its powers, and reaches the other butterflies'
+// twiddles through compile-time constants.
 template <class P, int S, bool Inv, bool Table>
 __device__ __forceinline__ void stage_compute(cf32 (&v)[P::E], int lane, const cf32* table)
 {
@@ -418,39 +428,31 @@ __device__ __forceinline__ void stage_compute(cf32 (&v)[P::E], int lane, const c
     constexpr int B = P::E / R;
     if constexpr (NS > 1) {
         const int k0 = lane & (NS - 1);
+        cf32 p[R];  // p[r] = w^(k0 r)
         if constexpr (Table) {
             static_assert(kTableN % SP == 0, "the table must cover the span");
-            constexpr int step = kTableN / SP;
-            static_for<0, B>([&](auto bi) {
-                constexpr int b = decltype(bi)::value;
-                const int k = k0 + (b * P::L) % NS;
-                static_for<1, R>([&](auto ri) {
-                    constexpr int r = decltype(ri)::value;
-                    const cf32 w = table[k * r * step];  // k r < SP: no wrap
-                    v[b * R + r] = cmul(v[b * R + r], Inv ? cconj(w) : w);
-                });
-            });
+            const cf32 w = table[k0 * (kTableN / SP)];  // k0 < SP: no wrap
+            p[1] = Inv ? cconj(w) : w;
         } else {
-            cf32 p[R];  // p[r] = w^(k0 r)
             p[1] = twiddle_of<SP, Inv>(k0);
-#pragma unroll
-            for (int r = 2; r < R; ++r) {
-                p[r] = (r % 2 == 0) ? cmul(p[r / 2], p[r / 2]) : cmul(p[r - 1], p[1]);
-            }
-            static_for<0, B>([&](auto bi) {
-                constexpr int b = decltype(bi)::value;
-                constexpr int kb = (b * P::L) % NS;
-                static_for<1, R>([&](auto ri) {
-                    constexpr int r = decltype(ri)::value;
-                    if constexpr (kb == 0) {
-                        v[b * R + r] = cmul(v[b * R + r], p[r]);
-                    } else {
-                        constexpr cf32 c = const_twiddle<Inv>(static_cast<long long>(kb) * r, SP);
-                        v[b * R + r] = cmul(cmul(v[b * R + r], c), p[r]);
-                    }
-                });
-            });
         }
+#pragma unroll
+        for (int r = 2; r < R; ++r) {
+            p[r] = (r % 2 == 0) ? cmul(p[r / 2], p[r / 2]) : cmul(p[r - 1], p[1]);
+        }
+        static_for<0, B>([&](auto bi) {
+            constexpr int b = decltype(bi)::value;
+            constexpr int kb = (b * P::L) % NS;
+            static_for<1, R>([&](auto ri) {
+                constexpr int r = decltype(ri)::value;
+                if constexpr (kb == 0) {
+                    v[b * R + r] = cmul(v[b * R + r], p[r]);
+                } else {
+                    constexpr cf32 c = const_twiddle<Inv>(static_cast<long long>(kb) * r, SP);
+                    v[b * R + r] = cmul(cmul(v[b * R + r], c), p[r]);
+                }
+            });
+        });
     }
 #pragma unroll
     for (int b = 0; b < B; ++b) {
@@ -587,12 +589,12 @@ struct Staged {
 // Transforms past the end of the batch still run the stages (on whatever is in registers) but
 // touch no global memory, so every lane reaches every barrier.
 template <class P, bool Inv, bool Table, class Io>
-__global__ void __launch_bounds__(kBlock) fft_kernel(Io io, long long batch, const cf32* table)
+__global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch, const cf32* table)
 {
     __shared__ cf32 lds[P::T * P::kStride];
 
     constexpr bool kWaveGroups = P::kWaveLocal && !Io::kGroupIsBlock;
-    constexpr int kGroupThreads = kWaveGroups ? 64 : kBlock;
+    constexpr int kGroupThreads = kWaveGroups ? 64 : P::kThreads;
     constexpr int kGroupT = kGroupThreads / P::L;  // transforms per group
     using Full = Group<kGroupT, kGroupThreads, true>;
     using Tail = Group<kGroupT, kGroupThreads, false>;

@@ -19,9 +19,13 @@ void check_size(int n, const char* who);
 void check_keep(int keep, int n, const char* who);
 void check_real_arguments(const void* real_side, const void* complex_side, int n, int batch,
                           int complex_row, int max_n, const char* who);
-// n = 2 real transforms (m = 1): the combine / prepare alone (real.cu).
-void r2c_postprocess(const cf32* z, cf32* y, int m, int batch, int keep, hipStream_t stream);
-void c2r_preprocess(const cf32* x, cf32* z, int m, int batch, int keep, hipStream_t stream);
+// n = 2 real transforms (m = 1, where the complex transform is the identity): the combine or
+// prepare alone, one row per lane (real.hip).
+void r2c_n2(const float* x, cf32* y, int batch, int keep, hipStream_t stream);
+void c2r_n2(const cf32* x, float* y, int batch, int keep, hipStream_t stream);
+// n = 4 inverse (m = 2) in closed form, one row per lane; false (nothing queued) when y is not
+// 16-byte aligned.
+bool c2r_n4(const cf32* x, float* y, int batch, int keep, hipStream_t stream);
 // The table of exp(-2 pi i m / kTableN) on the current device, built on first use.
 const cf32* twiddle_table();
 
@@ -33,7 +37,7 @@ void launch(const Io& io, long long batch, hipStream_t stream)
     const long long blocks = (batch + P::T - 1) / P::T;
     const cf32* table = Table ? twiddle_table() : nullptr;
     hipLaunchKernelGGL((fft_kernel<P, Inv, Table, Io>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kBlock), 0, stream, io, batch, table);
+                       dim3(P::kThreads), 0, stream, io, batch, table);
     SPX_LAUNCH_CHECK();
 }
 
@@ -43,7 +47,7 @@ void dispatch(int n, const Io& io, long long batch, hipStream_t stream)
     switch (n) {
 #define SPX_CASE(N)                                                          \
     case N:                                                                  \
-        launch<Plan<N, R, default_e<N>()>, Inv, Table>(io, batch, stream);   \
+        launch<Plan<N, R, default_e<N, R>()>, Inv, Table>(io, batch, stream);   \
         break;
         SPX_CASE(2)
         SPX_CASE(4)
@@ -275,7 +279,7 @@ struct Stockham {
         const int m = n / 2;
         const auto* z = reinterpret_cast<const cf32*>(x);
         if (m == 1) {
-            r2c_postprocess(z, y, 1, batch, keep, stream);
+            r2c_n2(x, y, batch, keep, stream);
             return;
         }
         dev::dispatch_dir<R, Table>(m, false, dev::R2cIo{z, y, keep}, batch, stream);
@@ -288,7 +292,10 @@ struct Stockham {
         const int m = n / 2;
         auto* z = reinterpret_cast<cf32*>(y);
         if (m == 1) {
-            c2r_preprocess(x, z, 1, batch, keep, stream);
+            c2r_n2(x, y, batch, keep, stream);
+            return;
+        }
+        if (m == 2 && c2r_n4(x, y, batch, keep, stream)) {
             return;
         }
         const float scale = 1.0f / static_cast<float>(m);

@@ -23,13 +23,14 @@ def ilog2(n: int) -> int:
     return max(0, math.ceil(math.log2(n))) if n > 1 else 0
 
 
-def default_e(n: int) -> int:
-    return min(n, 16)
+def default_e(n: int, radix: int) -> int:
+    """Values per lane (stockham.hpp: default_e): min(n, max(radix, 4, n / 256))."""
+    return min(n, max(radix, 4, n // BLOCK))
 
 
 def plan(n: int, radix: int, e: int | None = None) -> dict:
     """The stage radices and the lane split of an n-point transform with radix-`radix` stages."""
-    e = default_e(n) if e is None else e
+    e = default_e(n, radix) if e is None else e
     r = min(radix, n)
     full = ilog2(n) // ilog2(r)
     final = n >> (full * ilog2(r))
