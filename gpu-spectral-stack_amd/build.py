@@ -64,7 +64,8 @@ CAPI_SOURCES = [
     "registry.cpp",
     "capi.cpp",
 ]
-CAPI_HEADERS = ["spx_common.hpp", "stockham.hpp", "variant.hpp", "fft_api.hpp"]
+# Every header under csrc/ is a dependency of every object: a header edit recompiles them all.
+CAPI_HEADERS = sorted(p.name for p in CSRC.glob("*.hpp"))
 
 LIB = PKG / "libspectral_hip.so"
 EXT = PKG / "_C.so"

@@ -1,0 +1,317 @@
+#pragma once
+
+// Single-pass 2D real FFTs for arrays whose half spectrum fits in LDS: rfft2 / irfft2 and the
+// pruned FNO transforms (rfft2_modes / irfft2_modes) as ONE kernel and one HBM round trip per
+// array, where the row-then-column drivers (reference fft2d.cu:138-187, pruned.cu:172-209) need two
+// kernels and write the spectrum to HBM in between.
+//
+// A workgroup owns AP whole arrays (AP n1 n2 ~ 16384 points) and keeps each array's half spectrum
+// in an LDS tile of n1 rows by TS complex values (TS odd and > pad(n2/2), so a row can also hold a
+// padded row transform and the tile's columns fall in distinct banks):
+//
+//   forward  rows: each row of n2 reals is read as n2/2 complex values, transformed in registers
+//            (Stockham stages, exchanges in the tile row itself) and combined in place into its
+//            n2/2 + 1 bins; columns: the first w columns, transformed in place down the tile
+//            (element i of column c at tile[i TS + pad(c)]); store: the kept rows (all n1, or
+//            rows 0 .. m1-1 and n1-m1 .. n1-1) of those w columns, contiguous and coalesced.
+//   inverse  the mirror: load the kept rows and columns (zero elsewhere), inverse columns, then per
+//            row the c2r prepare, an inverse n2/2-point transform, and the real row stored.
+//
+// Normalization follows numpy: forward none, inverse 1 / (n1 n2) (the column and row scales are
+// folded into the row pass). The butterflies, twiddles and exchanges are the ones of stockham.hpp.
+
+#include "stockham.hpp"
+
+namespace spx::dev {
+
+// floor(x / d) by a multiply-high with m = ceil(2^32 / d): exact for x, d < 2^16 (the error term
+// x (m d - 2^32) / 2^32 < x d / 2^32 < 1 never reaches the next integer).
+struct FastDiv {
+    unsigned d;
+    unsigned long long m;
+
+    static FastDiv of(unsigned d)
+    {
+        return {d, ((1ULL << 32) + d - 1) / d};
+    }
+    __device__ __forceinline__ unsigned div(unsigned x) const
+    {
+        return static_cast<unsigned>((static_cast<unsigned long long>(x) * m) >> 32);
+    }
+};
+
+template <int N1_, int M_, int R, bool Table>
+struct Fused2d {
+    static constexpr int N1 = N1_;                 // rows (column transform length)
+    static constexpr int M = M_;                   // complex values per real row (n2 / 2)
+    static constexpr int N2 = 2 * M;
+    static constexpr bool kTable = Table;
+    using PR = Plan<M, R, default_e<M, R>()>;     // row transforms
+    using PC = Plan<N1, R, default_e<N1, R>()>;   // column transforms
+    static constexpr int TS = (pad(M) + 1) | 1;    // tile row stride, odd
+    static constexpr int kTile = N1 * TS;          // complex values per array
+    static constexpr int AP = cmax(1, 16384 / (N1 * N2));  // arrays per workgroup
+    static constexpr int NT = 512;                 // lanes per workgroup
+    static constexpr int NW = NT / 64;
+    static constexpr int kRows = AP * N1;
+    static constexpr int RPP = NT / PR::L;         // rows per pass
+    static constexpr int CPP = NT / PC::L;         // columns per pass
+    static constexpr int kMaxLoads = (AP * N1 * (M + 1) + NT - 1) / NT;  // inverse: loads per lane
+
+    static_assert(PR::L <= 64 && PC::L <= 64, "row and column transforms stay inside a wave");
+    static_assert(kRows % RPP == 0, "row passes cover the rows exactly");
+    static_assert(AP * kTile * sizeof(cf32) <= 80 * 1024, "tile exceeds the LDS budget");
+
+    // Tile row holding frequency-row f of the kept rows (all rows when m1 = 0).
+    __device__ __forceinline__ static int row_of(int f, int m1)
+    {
+        return (m1 > 0 && f >= m1) ? f + N1 - 2 * m1 : f;
+    }
+};
+
+// Combine of the real forward transform for one row held in place at s (Padded): pair k reads
+// Z[k] and Z[M-k] and writes X[k] and X[M-k] into the same slots (X[M] into slot M for k = 0).
+template <int M>
+__device__ __forceinline__ void combine_row(cf32* s, int k)
+{
+    const cf32 zk = s[pad(k & (M - 1))];
+    const cf32 zm = s[pad((M - k) & (M - 1))];
+    const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
+    const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
+    const cf32 wo = cmul(twiddle_of<2 * M, false>(k), od);
+    s[pad(k)] = cadd(ev, wo);
+    if (k < M - k) {
+        s[pad(M - k)] = cconj(csub(ev, wo));
+    }
+}
+
+// Prepare of the real inverse transform for one row in place at s (Padded): X[k] for k < w, zero
+// beyond; imaginary parts of X[0] and X[M] dropped.
+template <int M>
+__device__ __forceinline__ void prepare_row(cf32* s, int k, int w)
+{
+    cf32 xk = k < w ? s[pad(k)] : czero();
+    cf32 xm = M - k < w ? s[pad(M - k)] : czero();
+    if (k == 0) {
+        xk.im = 0.0f;
+        xm.im = 0.0f;
+    }
+    const cf32 ev{0.5f * (xk.re + xm.re), 0.5f * (xk.im - xm.im)};
+    const cf32 d{0.5f * (xk.re - xm.re), 0.5f * (xk.im + xm.im)};
+    const cf32 od = cmul(d, twiddle_of<2 * M, true>(k));
+    const cf32 iod{-od.im, od.re};
+    if (k < M) {
+        s[pad(k)] = cadd(ev, iod);
+    }
+    if (k > 0 && k < M - k) {
+        s[pad(M - k)] = cconj(csub(ev, iod));
+    }
+}
+
+// Forward: z = the real arrays viewed as complex (batch x N1 x M), y = batch arrays of rows_out x w
+// values (rows_out = 2 m1 when m1 > 0, else N1).
+template <class F>
+__global__ void __launch_bounds__(F::NT)
+    rfft2_fused_kernel(const cf32* __restrict__ z, cf32* __restrict__ y, int m1, int w,
+                       FastDiv wdiv, long long batch, const cf32* table)
+{
+    using PR = typename F::PR;
+    using PC = typename F::PC;
+    __shared__ cf32 tile[F::AP * F::kTile];
+
+    const long long first = static_cast<long long>(blockIdx.x) * F::AP;
+    const int count = static_cast<int>(batch - first < F::AP ? batch - first : F::AP);
+    const int tid = threadIdx.x;
+
+    // Rows: load straight from HBM, transform, combine in place.
+#pragma unroll 1
+    for (int p = 0; p < F::kRows / F::RPP; ++p) {
+        const int row = p * F::RPP + tid / PR::L;  // row of the workgroup's arrays
+        const int lane = tid % PR::L;
+        const int a = row / F::N1;
+        cf32* const s = tile + a * F::kTile + (row % F::N1) * F::TS;
+        cf32 v[PR::E];
+        if (a < count) {
+            const cf32* src = z + (first * F::N1 + row) * F::M;
+#pragma unroll
+            for (int b = 0; b < PR::E / PR::template radix<0>(); ++b) {
+#pragma unroll
+                for (int r = 0; r < PR::template radix<0>(); ++r) {
+                    v[b * PR::template radix<0>() + r] = src[input_index<PR, 0>(lane, b, r)];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < PR::E; ++e) {
+                v[e] = czero();
+            }
+        }
+        run_stages<PR, 0, false, F::kTable>(v, s, lane, table);
+        lds_sync<true>();
+        final_write<PR>(s, v, lane);
+        lds_sync<true>();
+        for (int k = lane; k <= F::M / 2; k += PR::L) {
+            combine_row<F::M>(s, k);
+        }
+    }
+    __syncthreads();
+
+    // Columns 0 .. w-1 of every array, in place down the tile.
+    const int total_cols = F::AP * w;
+#pragma unroll 1
+    for (int c0 = 0; c0 < total_cols; c0 += F::CPP) {
+        const int cg = c0 + tid / PC::L;
+        const int lane = tid % PC::L;
+        if (cg < total_cols) {
+            const int a = static_cast<int>(wdiv.div(static_cast<unsigned>(cg)));
+            const int c = cg - a * w;
+            cf32* const s = tile + a * F::kTile + pad(c);
+            cf32 v[PC::E];
+            stage_read<PC, 0, Strided<F::TS>>(s, v, lane);
+            run_stages<PC, 0, false, F::kTable, Strided<F::TS>>(v, s, lane, table);
+            lds_sync<true>();
+            final_write<PC, Strided<F::TS>>(s, v, lane);
+        }
+    }
+    __syncthreads();
+
+    // Store the kept rows of the first w columns: one wave per output row, lanes along the row.
+    const int rows_out = m1 > 0 ? 2 * m1 : F::N1;
+    const int wave = tid / 64;
+    const int lane = tid % 64;
+    for (int a = 0; a < count; ++a) {
+        cf32* const dst = y + (first + a) * rows_out * w;
+        for (int f = wave; f < rows_out; f += F::NW) {
+            const cf32* src = tile + a * F::kTile + F::row_of(f, m1) * F::TS;
+            for (int c = lane; c < w; c += 64) {
+                st_stream(dst + f * w + c, src[pad(c)]);
+            }
+        }
+    }
+}
+
+// Inverse: x = batch arrays of rows_in x w values (rows_in = 2 m1 when m1 > 0, else N1; the other
+// frequencies are zero), z = the real outputs viewed as complex (batch x N1 x M). wdiv divides by
+// w, adiv by rows_in w.
+template <class F>
+__global__ void __launch_bounds__(F::NT)
+    irfft2_fused_kernel(const cf32* __restrict__ x, cf32* __restrict__ z, int m1, int w,
+                        FastDiv wdiv, FastDiv adiv, long long batch, const cf32* table)
+{
+    using PR = typename F::PR;
+    using PC = typename F::PC;
+    __shared__ cf32 tile[F::AP * F::kTile];
+
+    const long long first = static_cast<long long>(blockIdx.x) * F::AP;
+    const int count = static_cast<int>(batch - first < F::AP ? batch - first : F::AP);
+    const int tid = threadIdx.x;
+    const int wave = tid / 64;
+    const int lane64 = tid % 64;
+
+    // Load the kept rows of the first w columns (contiguous in x: count arrays of rows_in x w),
+    // every lane's loads in flight before any LDS write; then zero the dropped rows.
+    const int rows_in = m1 > 0 ? 2 * m1 : F::N1;
+    const int per_array = rows_in * w;
+    const int total = count * per_array;
+    const cf32* const src = x + first * per_array;
+    cf32 val[F::kMaxLoads];
+#pragma unroll
+    for (int k = 0; k < F::kMaxLoads; ++k) {
+        const int e = tid + k * F::NT;
+        val[k] = e < total ? src[e] : czero();
+    }
+#pragma unroll
+    for (int k = 0; k < F::kMaxLoads; ++k) {
+        const int e = tid + k * F::NT;
+        if (e < total) {
+            const int a = static_cast<int>(adiv.div(static_cast<unsigned>(e)));
+            const int rem = e - a * per_array;
+            const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(rem)));
+            const int c = rem - f * w;
+            tile[a * F::kTile + F::row_of(f, m1) * F::TS + pad(c)] = val[k];
+        }
+    }
+    if (m1 > 0) {
+        for (int a = 0; a < count; ++a) {
+            for (int i = m1 + wave; i < F::N1 - m1; i += F::NW) {
+                cf32* const d = tile + a * F::kTile + i * F::TS;
+                for (int c = lane64; c < w; c += 64) {
+                    d[pad(c)] = czero();
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // Inverse columns 0 .. w-1, in place.
+    const int total_cols = F::AP * w;
+#pragma unroll 1
+    for (int c0 = 0; c0 < total_cols; c0 += F::CPP) {
+        const int cg = c0 + tid / PC::L;
+        const int lane = tid % PC::L;
+        if (cg < total_cols) {
+            const int a = static_cast<int>(wdiv.div(static_cast<unsigned>(cg)));
+            const int c = cg - a * w;
+            cf32* const s = tile + a * F::kTile + pad(c);
+            cf32 v[PC::E];
+            stage_read<PC, 0, Strided<F::TS>>(s, v, lane);
+            run_stages<PC, 0, true, F::kTable, Strided<F::TS>>(v, s, lane, table);
+            lds_sync<true>();
+            final_write<PC, Strided<F::TS>>(s, v, lane);
+        }
+    }
+    __syncthreads();
+
+    // Rows: prepare in place, inverse transform, store the real row (scale 1 / (N1 M) covers
+    // both passes: the prepare's halves make 1 / M the row inverse of numpy's irfft).
+    constexpr float scale = 1.0f / static_cast<float>(F::N1 * F::M);
+#pragma unroll 1
+    for (int p = 0; p < F::kRows / F::RPP; ++p) {
+        const int row = p * F::RPP + tid / PR::L;
+        const int lane = tid % PR::L;
+        const int a = row / F::N1;
+        cf32* const s = tile + a * F::kTile + (row % F::N1) * F::TS;
+        for (int k = lane; k <= F::M / 2; k += PR::L) {
+            prepare_row<F::M>(s, k, w);
+        }
+        lds_sync<true>();
+        cf32 v[PR::E];
+        stage_read<PR, 0>(s, v, lane);
+        run_stages<PR, 0, true, F::kTable>(v, s, lane, table);
+        if constexpr (PR::L >= 16) {
+            // Rows of 16 lanes or more: every store is a run of at least 128 bytes.
+            if (a < count) {
+                cf32* const dst = z + (first * F::N1 + row) * F::M;
+                constexpr int RL = PR::template radix<PR::kStages - 1>();
+#pragma unroll
+                for (int b = 0; b < PR::E / RL; ++b) {
+#pragma unroll
+                    for (int r = 0; r < RL; ++r) {
+                        st_stream(dst + lane + b * PR::L + r * (PR::N / RL),
+                                  cscale(v[b * RL + r], scale));
+                    }
+                }
+            }
+        } else {
+            // Short rows: back to the tile row, then each wave stores its 64 / L consecutive rows
+            // (consecutive in z too) as one contiguous run.
+            lds_sync<true>();
+            final_write<PR>(s, v, lane);
+            lds_sync<true>();
+            const int row0 = p * F::RPP + (tid / 64) * (64 / PR::L);
+#pragma unroll
+            for (int k = 0; k < PR::E; ++k) {
+                const int e = tid % 64 + k * 64;
+                const int rw = row0 + e / F::M;
+                const int i = e % F::M;
+                const int aw = rw / F::N1;
+                if (aw < count) {
+                    st_stream(z + (first * F::N1 + rw) * F::M + i,
+                              cscale(tile[aw * F::kTile + (rw % F::N1) * F::TS + pad(i)], scale));
+                }
+            }
+        }
+    }
+}
+
+}  // namespace spx::dev

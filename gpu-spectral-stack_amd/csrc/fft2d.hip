@@ -89,6 +89,12 @@ std::size_t real_work(const FftImpl& impl, int n1, int n2, int batch)
     return impl.real_needs_work ? count(n1, n2 / 2, batch) : 0;
 }
 
+// The strided method runs as one single-pass kernel when the implementation has one for the shape.
+bool fused(const FftImpl& impl, Columns columns, int n1, int n2)
+{
+    return columns == Columns::Strided && impl.fused != nullptr && impl.fused->supports(n1, n2);
+}
+
 }  // namespace
 
 void transpose(const cf32* x, cf32* y, int rows, int cols, int batch, hipStream_t stream)
@@ -128,6 +134,9 @@ void fft2_c2c(const FftImpl& impl, Columns columns, const cf32* x, cf32* y, int 
 
 std::size_t fft2_r2c_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch)
 {
+    if (fused(impl, columns, n1, n2)) {
+        return 0;
+    }
     const std::size_t half = columns == Columns::Strided ? 0 : 2 * count(n1, n2 / 2 + 1, batch);
     return half + real_work(impl, n1, n2, batch);
 }
@@ -137,6 +146,10 @@ void fft2_r2c(const FftImpl& impl, Columns columns, const float* x, cf32* y, int
 {
     check(impl, columns, n1, n2, batch, true);
     const int w = n2 / 2 + 1;
+    if (fused(impl, columns, n1, n2)) {
+        impl.fused->r2c(x, y, n1, n2, 0, w, batch, stream);
+        return;
+    }
     if (columns == Columns::Strided) {
         cf32* rwork = impl.real_needs_work ? work : nullptr;
         impl.r2c(x, y, n2, batch * n1, rwork, stream);
@@ -154,6 +167,9 @@ void fft2_r2c(const FftImpl& impl, Columns columns, const float* x, cf32* y, int
 
 std::size_t fft2_c2r_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch)
 {
+    if (fused(impl, columns, n1, n2)) {
+        return 0;
+    }
     const std::size_t q = count(n1, n2 / 2 + 1, batch);
     return (columns == Columns::Strided ? q : 2 * q) + real_work(impl, n1, n2, batch);
 }
@@ -163,6 +179,10 @@ void fft2_c2r(const FftImpl& impl, Columns columns, const cf32* x, float* y, int
 {
     check(impl, columns, n1, n2, batch, true);
     const int w = n2 / 2 + 1;
+    if (fused(impl, columns, n1, n2)) {
+        impl.fused->c2r(x, y, n1, n2, 0, w, batch, stream);
+        return;
+    }
     const std::size_t q = count(n1, w, batch);
     if (columns == Columns::Strided) {
         // Columns first, out of place (the input is the caller's), then the real rows.

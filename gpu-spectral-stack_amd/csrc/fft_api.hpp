@@ -35,6 +35,18 @@ struct PrunedFns {
                     Direction direction, hipStream_t stream);
 };
 
+// Single-pass 2D real transforms for the shapes whose half spectrum fits in LDS (fft2_fused.hpp):
+// one kernel and one HBM round trip instead of a row pass and a column pass. They keep rows 0 ..
+// n1-1 (m1 = 0) or 0 .. m1-1 and n1-m1 .. n1-1 (m1 > 0), and columns 0 .. w-1 of the half
+// spectrum; the inverse reads that layout with every other frequency zero.
+struct Fused2dFns {
+    bool (*supports)(int n1, int n2);
+    void (*r2c)(const float* x, cf32* y, int n1, int n2, int m1, int w, int batch,
+                hipStream_t stream);
+    void (*c2r)(const cf32* x, float* y, int n1, int n2, int m1, int w, int batch,
+                hipStream_t stream);
+};
+
 // One implementation, by name (reference registry.hpp:14-25).
 struct FftImpl {
     const char* name;
@@ -47,6 +59,7 @@ struct FftImpl {
     int max_c2c_n;            // largest 1D complex transform
     int max_real_n;           // largest real transform
     bool real_needs_work;     // r2c and c2r use the work buffer
+    const Fused2dFns* fused;  // single-pass 2D kernels, or nullptr
 };
 
 // The registry, in the reference's order (registry.hpp:28-40).
@@ -106,7 +119,8 @@ void scatter_modes(const cf32* modes, cf32* full, int n1, int w, int m1, int m2,
     void c2r_##NAME(const cf32* x, float* y, int n, int batch, cf32* work, hipStream_t stream); \
     void columns_##NAME(const cf32* x, cf32* y, int n, int cols, int slabs,                    \
                         Direction direction, hipStream_t stream);                               \
-    extern const PrunedFns pruned_##NAME;
+    extern const PrunedFns pruned_##NAME;                                                      \
+    extern const Fused2dFns fused_##NAME;
 
 namespace spx {
 SPX_DECLARE_VARIANT(stockham_r2)

@@ -167,8 +167,21 @@ void fft_c2c_pruned(const FftImpl& impl, const cf32* x, cf32* y, int n, int keep
     }
 }
 
+namespace {
+
+// One single-pass kernel when the implementation has one for the shape.
+bool fused(const FftImpl& impl, int n1, int n2)
+{
+    return impl.fused != nullptr && impl.fused->supports(n1, n2);
+}
+
+}  // namespace
+
 std::size_t rfft2_modes_workspace(const FftImpl& impl, int n1, int n2, int, int m2, int batch)
 {
+    if (fused(impl, n1, n2)) {
+        return 0;  // one single-pass kernel
+    }
     if (impl.pruned != nullptr) {
         return count(n1, m2, batch);  // the row transforms' m2 columns
     }
@@ -180,6 +193,10 @@ void rfft2_modes(const FftImpl& impl, const float* x, cf32* modes, int n1, int n
                  int m2, int batch, cf32* work, hipStream_t stream)
 {
     check_2d(impl, n1, n2, m1, m2, batch);
+    if (fused(impl, n1, n2)) {
+        impl.fused->r2c(x, modes, n1, n2, m1, m2, batch, stream);
+        return;
+    }
     if (impl.pruned != nullptr) {
         impl.pruned->r2c(x, work, n2, batch * n1, m2, stream);  // n1 x m2 per array
         impl.pruned->columns(work, modes, n1, m2, batch, 0, m1, Direction::Forward, stream);
@@ -193,6 +210,9 @@ void rfft2_modes(const FftImpl& impl, const float* x, cf32* modes, int n1, int n
 
 std::size_t irfft2_modes_workspace(const FftImpl& impl, int n1, int n2, int, int m2, int batch)
 {
+    if (fused(impl, n1, n2)) {
+        return 0;
+    }
     if (impl.pruned != nullptr) {
         return count(n1, m2, batch);
     }
@@ -204,6 +224,10 @@ void irfft2_modes(const FftImpl& impl, const cf32* modes, float* y, int n1, int 
                   int m2, int batch, cf32* work, hipStream_t stream)
 {
     check_2d(impl, n1, n2, m1, m2, batch);
+    if (fused(impl, n1, n2)) {
+        impl.fused->c2r(modes, y, n1, n2, m1, m2, batch, stream);
+        return;
+    }
     if (impl.pruned != nullptr) {
         impl.pruned->columns(modes, work, n1, m2, batch, m1, 0, Direction::Inverse, stream);
         impl.pruned->c2r(work, y, n2, batch * n1, m2, stream);  // columns m2.. are zero

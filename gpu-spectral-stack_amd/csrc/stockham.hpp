@@ -319,14 +319,15 @@ constexpr int kTableN = 4096;
 
 // --- plans ----------------------------------------------------------------------------------
 
-// N-point transform, stages of radix R (then one stage of the leftover factor), E values per lane.
-template <int N_, int R_, int E_>
+// N-point transform, stages of radix R (then one stage of the leftover factor), E values per lane,
+// Threads lanes per workgroup (0: 256, or L when one transform needs more).
+template <int N_, int R_, int E_, int Threads_ = 0>
 struct Plan {
     static constexpr int N = N_;
     static constexpr int R = R_ < N_ ? R_ : N_;
     static constexpr int E = E_;
     static constexpr int L = N / E;                         // lanes per transform
-    static constexpr int kThreads = L > kBlock ? L : kBlock;  // lanes per workgroup
+    static constexpr int kThreads = Threads_ > 0 ? Threads_ : (L > kBlock ? L : kBlock);
     static constexpr int T = kThreads / L;                    // transforms per workgroup
     static constexpr int kFull = clog2(N) / clog2(R);       // radix-R stages
     static constexpr int kFinal = N >> (kFull * clog2(R));  // leftover radix (1: none)
@@ -336,6 +337,7 @@ struct Plan {
 
     static_assert(N >= 2 && (N & (N - 1)) == 0, "N must be a power of two");
     static_assert(E <= N && N % E == 0 && L <= kMaxBlock, "bad lane split");
+    static_assert(kThreads % L == 0 && kThreads <= kMaxBlock, "bad workgroup size");
     static_assert(R <= E && kFinal <= E, "a lane must hold a whole butterfly");
 
     template <int S>
@@ -355,6 +357,28 @@ constexpr int default_e()
     return cmin(N, cmax(cmax(R, 4), N / kBlock));
 }
 
+// Strided columns (StridedIo) stage T neighbouring columns per workgroup, so every row access is a
+// run of T * 8 bytes: T = 16 (128-byte runs) up to N = 512; beyond, T shrinks to keep the column
+// tile near 70 KB of LDS (two workgroups per CU). E grows with T so a workgroup stays within 1024
+// lanes.
+template <int N>
+constexpr int column_t()
+{
+    return N <= 512 ? 16 : 8192 / N;
+}
+
+template <int N, int R>
+constexpr int column_e()
+{
+    return cmax(default_e<N, R>(), cmin(N, N * column_t<N>() / kMaxBlock));
+}
+
+template <int N, int R>
+constexpr int column_threads()
+{
+    return cmax(kBlock, column_t<N>() * (N / column_e<N, R>()));
+}
+
 // --- synchronization ------------------------------------------------------------------------
 
 template <bool WaveLocal>
@@ -371,19 +395,32 @@ __device__ __forceinline__ void lds_sync()
 
 // --- stage pieces ---------------------------------------------------------------------------
 //
-// LDS addresses are a per-lane base plus a compile-time offset: pad(a + c) = pad(a) + pad(c)
-// whenever the low four bits of a and c add without a carry, and for every access pattern below
-// that holds for all lanes (power-of-two strides, lane < L). `splits` checks it exhaustively at
-// compile time for each instantiated plan and stage, so a plan where it failed would not build.
+// A transform's values sit in LDS in one of two layouts: element i at s[Lay::at(i)].
+//   Padded       one complex of padding after every 16 (a transform stored as a row)
+//   Strided<ST>  every ST values (a column of a row-major tile whose rows are ST long)
+// LDS addresses are a per-lane base plus a compile-time offset. For Strided that is linearity;
+// for Padded, pad(a + c) = pad(a) + pad(c) whenever the low four bits of a and c add without a
+// carry, and for every access pattern below that holds for all lanes (power-of-two strides,
+// lane < L). read_splits / write_splits check it exhaustively at compile time for each
+// instantiated plan, stage and layout, so a plan where it failed would not build.
 
-template <class P>
+struct Padded {
+    __host__ __device__ static constexpr int at(int i) { return pad(i); }
+};
+
+template <int Stride>
+struct Strided {
+    __host__ __device__ static constexpr int at(int i) { return i * Stride; }
+};
+
+template <class P, class Lay>
 constexpr bool read_splits(int R)
 {
     for (int lane = 0; lane < P::L; ++lane) {
         for (int b = 0; b < P::E / R; ++b) {
             for (int r = 0; r < R; ++r) {
                 const int off = b * P::L + r * (P::N / R);
-                if (pad(lane + off) != pad(lane) + pad(off)) {
+                if (Lay::at(lane + off) != Lay::at(lane) + Lay::at(off)) {
                     return false;
                 }
             }
@@ -392,7 +429,7 @@ constexpr bool read_splits(int R)
     return true;
 }
 
-template <class P>
+template <class P, class Lay>
 constexpr bool write_splits(int R, int NS)
 {
     for (int lane = 0; lane < P::L; ++lane) {
@@ -405,7 +442,7 @@ constexpr bool write_splits(int R, int NS)
                 const int j = lane + b * P::L;  // the definition: k = j mod NS
                 const int k = j & (NS - 1);
                 if ((j - k) * R + k + r * NS != base + off
-                    || pad(base + off) != pad(base) + pad(off)) {
+                    || Lay::at(base + off) != Lay::at(base) + Lay::at(off)) {
                     return false;
                 }
             }
@@ -462,36 +499,36 @@ __device__ __forceinline__ void stage_compute(cf32 (&v)[P::E], int lane, const c
 
 // Stage S's outputs to their Stockham positions in LDS: output r of butterfly j goes to
 // (j - k) R + k + r NS.
-template <class P, int S>
+template <class P, int S, class Lay = Padded>
 __device__ __forceinline__ void stage_write(cf32* s, const cf32 (&v)[P::E], int lane)
 {
     constexpr int R = P::template radix<S>();
     constexpr int NS = P::template span_before<S>();
-    static_assert(write_splits<P>(R, NS), "LDS offsets do not split for this plan");
+    static_assert(write_splits<P, Lay>(R, NS), "LDS offsets do not split for this plan");
     const int k0 = lane & (NS - 1);
-    cf32* const base = s + pad((lane - k0) * R + k0);
+    cf32* const base = s + Lay::at((lane - k0) * R + k0);
     static_for<0, P::E / R>([&](auto bi) {
         constexpr int b = decltype(bi)::value;
         constexpr int kb = (b * P::L) % NS;
         static_for<0, R>([&](auto ri) {
             constexpr int r = decltype(ri)::value;
-            base[pad((b * P::L - kb) * R + kb + r * NS)] = v[b * R + r];
+            base[Lay::at((b * P::L - kb) * R + kb + r * NS)] = v[b * R + r];
         });
     });
 }
 
 // Stage S's inputs from LDS: v[b R + r] = s[j + r N / R], j = lane + b L.
-template <class P, int S>
+template <class P, int S, class Lay = Padded>
 __device__ __forceinline__ void stage_read(const cf32* s, cf32 (&v)[P::E], int lane)
 {
     constexpr int R = P::template radix<S>();
-    static_assert(read_splits<P>(R), "LDS offsets do not split for this plan");
-    const cf32* const base = s + pad(lane);
+    static_assert(read_splits<P, Lay>(R), "LDS offsets do not split for this plan");
+    const cf32* const base = s + Lay::at(lane);
     static_for<0, P::E / R>([&](auto bi) {
         constexpr int b = decltype(bi)::value;
         static_for<0, R>([&](auto ri) {
             constexpr int r = decltype(ri)::value;
-            v[b * R + r] = base[pad(b * P::L + r * (P::N / R))];
+            v[b * R + r] = base[Lay::at(b * P::L + r * (P::N / R))];
         });
     });
 }
@@ -505,31 +542,31 @@ __device__ __forceinline__ constexpr int input_index(int lane, int b, int r)
 
 // Runs stages S .. kStages-1. On entry v holds stage S's inputs; on exit the last stage's
 // outputs, output r of butterfly b being element lane + b L + r N / R_last.
-template <class P, int S, bool Inv, bool Table>
+template <class P, int S, bool Inv, bool Table, class Lay = Padded>
 __device__ __forceinline__ void run_stages(cf32 (&v)[P::E], cf32* s, int lane, const cf32* table)
 {
     stage_compute<P, S, Inv, Table>(v, lane, table);
     if constexpr (S + 1 < P::kStages) {
         lds_sync<P::kWaveLocal>();  // every lane has read the previous contents of s
-        stage_write<P, S>(s, v, lane);
+        stage_write<P, S, Lay>(s, v, lane);
         lds_sync<P::kWaveLocal>();
-        stage_read<P, S + 1>(s, v, lane);
-        run_stages<P, S + 1, Inv, Table>(v, s, lane, table);
+        stage_read<P, S + 1, Lay>(s, v, lane);
+        run_stages<P, S + 1, Inv, Table, Lay>(v, s, lane, table);
     }
 }
 
 // Writes the last stage's outputs to LDS in natural order (for a staged store).
-template <class P>
+template <class P, class Lay = Padded>
 __device__ __forceinline__ void final_write(cf32* s, const cf32 (&v)[P::E], int lane)
 {
     constexpr int R = P::template radix<P::kStages - 1>();
-    static_assert(read_splits<P>(R), "LDS offsets do not split for this plan");
-    cf32* const base = s + pad(lane);
+    static_assert(read_splits<P, Lay>(R), "LDS offsets do not split for this plan");
+    cf32* const base = s + Lay::at(lane);
     static_for<0, P::E / R>([&](auto bi) {
         constexpr int b = decltype(bi)::value;
         static_for<0, R>([&](auto ri) {
             constexpr int r = decltype(ri)::value;
-            base[pad(b * P::L + r * (P::N / R))] = v[b * R + r];
+            base[Lay::at(b * P::L + r * (P::N / R))] = v[b * R + r];
         });
     });
 }

@@ -7,6 +7,7 @@
 // The checks and their messages follow the reference's drivers (stockham.cuh:489-620,
 // real.cu:160-180, fourstep.cuh:110-131): callers and tests match on them.
 
+#include "fft2_fused.hpp"
 #include "fft_api.hpp"
 #include "stockham.hpp"
 
@@ -48,6 +49,34 @@ void dispatch(int n, const Io& io, long long batch, hipStream_t stream)
 #define SPX_CASE(N)                                                          \
     case N:                                                                  \
         launch<Plan<N, R, default_e<N, R>()>, Inv, Table>(io, batch, stream);   \
+        break;
+        SPX_CASE(2)
+        SPX_CASE(4)
+        SPX_CASE(8)
+        SPX_CASE(16)
+        SPX_CASE(32)
+        SPX_CASE(64)
+        SPX_CASE(128)
+        SPX_CASE(256)
+        SPX_CASE(512)
+        SPX_CASE(1024)
+        SPX_CASE(2048)
+        SPX_CASE(4096)
+#undef SPX_CASE
+    default:
+        throw InvalidArgument("stockham: unsupported size " + str(n));
+    }
+}
+
+// Strided columns: the plans of column_e / column_threads.
+template <int R, bool Inv, bool Table, class Io>
+void dispatch_columns(int n, const Io& io, long long batch, hipStream_t stream)
+{
+    switch (n) {
+#define SPX_CASE(N)                                                                          \
+    case N:                                                                                  \
+        launch<Plan<N, R, column_e<N, R>(), column_threads<N, R>()>, Inv, Table>(io, batch,   \
+                                                                               stream);      \
         break;
         SPX_CASE(2)
         SPX_CASE(4)
@@ -262,8 +291,12 @@ struct Stockham {
         }
         const bool inverse = direction == Direction::Inverse;
         const float scale = inverse ? 1.0f / static_cast<float>(n) : 1.0f;
-        dev::dispatch_dir<R, Table>(n, inverse, dev::StridedIo{x, y, cols, scale, m1_in, m1_out},
-                                    batch, stream);
+        const dev::StridedIo io{x, y, cols, scale, m1_in, m1_out};
+        if (inverse) {
+            dev::dispatch_columns<R, true, Table>(n, io, batch, stream);
+        } else {
+            dev::dispatch_columns<R, false, Table>(n, io, batch, stream);
+        }
     }
 
     static void columns(const cf32* x, cf32* y, int n, int cols, int slabs, Direction direction,
@@ -344,6 +377,113 @@ struct Stockham {
     }
 };
 
+// The (n1, n2) shapes with a single-pass 2D kernel: both in 32 .. 256 and the half spectrum (plus
+// row padding) within the 80 KB LDS tile of fft2_fused.hpp.
+#define SPX_FUSED_SHAPES(X)                                                                     \
+    X(32, 32) X(64, 32) X(128, 32) X(256, 32) X(32, 64) X(64, 64) X(128, 64) X(256, 64)         \
+    X(32, 128) X(64, 128) X(128, 128) X(32, 256) X(64, 256)
+
+// Single-pass 2D drivers of one variant (radix 4 and up; radix 2 has none).
+template <int R, bool Table>
+struct Fused2dDriver {
+    static bool supports(int n1, int n2)
+    {
+        if constexpr (R >= 4) {
+#define SPX_X(A, B)                 \
+    if (n1 == (A) && n2 == (B)) {   \
+        return true;                \
+    }
+            SPX_FUSED_SHAPES(SPX_X)
+#undef SPX_X
+        }
+        (void)n1;
+        (void)n2;
+        return false;
+    }
+
+    static void check(const void* real_side, const void* complex_side, int n1, int n2, int m1,
+                      int w, int batch)
+    {
+        if (!supports(n1, n2)) {
+            throw InvalidArgument("fused 2D: no kernel for " + str(n1) + " x " + str(n2));
+        }
+        if (batch < 1 || m1 < 0 || 2 * m1 > n1 || w < 1 || w > n2 / 2 + 1) {
+            throw InvalidArgument("fused 2D: bad batch, m1 or w");
+        }
+        const auto* r = static_cast<const char*>(real_side);
+        const auto* c = static_cast<const char*>(complex_side);
+        const std::size_t real_bytes =
+            static_cast<std::size_t>(batch) * static_cast<std::size_t>(n1) * n2 * sizeof(float);
+        const std::size_t complex_bytes = static_cast<std::size_t>(batch)
+                                          * static_cast<std::size_t>(m1 > 0 ? 2 * m1 : n1) * w
+                                          * sizeof(cf32);
+        if (r < c + complex_bytes && c < r + real_bytes) {
+            throw InvalidArgument("fused 2D: input and output must not overlap");
+        }
+    }
+
+    template <int N1, int M>
+    static void launch_r2c(const float* x, cf32* y, int m1, int w, int batch, hipStream_t stream)
+    {
+        using F = dev::Fused2d<N1, M, R, Table>;
+        const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
+        const cf32* table = Table ? twiddle_table() : nullptr;
+        hipLaunchKernelGGL((dev::rfft2_fused_kernel<F>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(F::NT), 0, stream, reinterpret_cast<const cf32*>(x), y, m1, w,
+                           dev::FastDiv::of(static_cast<unsigned>(w)),
+                           static_cast<long long>(batch), table);
+        SPX_LAUNCH_CHECK();
+    }
+
+    template <int N1, int M>
+    static void launch_c2r(const cf32* x, float* y, int m1, int w, int batch, hipStream_t stream)
+    {
+        using F = dev::Fused2d<N1, M, R, Table>;
+        const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
+        const cf32* table = Table ? twiddle_table() : nullptr;
+        const int rows_in = m1 > 0 ? 2 * m1 : N1;
+        hipLaunchKernelGGL((dev::irfft2_fused_kernel<F>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(F::NT), 0, stream, x, reinterpret_cast<cf32*>(y), m1, w,
+                           dev::FastDiv::of(static_cast<unsigned>(w)),
+                           dev::FastDiv::of(static_cast<unsigned>(rows_in * w)),
+                           static_cast<long long>(batch), table);
+        SPX_LAUNCH_CHECK();
+    }
+
+    static void r2c(const float* x, cf32* y, int n1, int n2, int m1, int w, int batch,
+                    hipStream_t stream)
+    {
+        check(x, y, n1, n2, m1, w, batch);
+        if constexpr (R >= 4) {
+#define SPX_X(A, B)                                                  \
+    if (n1 == (A) && n2 == (B)) {                                    \
+        launch_r2c<(A), (B) / 2>(x, y, m1, w, batch, stream);        \
+        return;                                                      \
+    }
+            SPX_FUSED_SHAPES(SPX_X)
+#undef SPX_X
+        }
+    }
+
+    // Not constexpr, like Stockham::pruned_fns: host function addresses only.
+    static Fused2dFns fns() { return {&supports, &r2c, &c2r}; }
+
+    static void c2r(const cf32* x, float* y, int n1, int n2, int m1, int w, int batch,
+                    hipStream_t stream)
+    {
+        check(y, x, n1, n2, m1, w, batch);
+        if constexpr (R >= 4) {
+#define SPX_X(A, B)                                                  \
+    if (n1 == (A) && n2 == (B)) {                                    \
+        launch_c2r<(A), (B) / 2>(x, y, m1, w, batch, stream);        \
+        return;                                                      \
+    }
+            SPX_FUSED_SHAPES(SPX_X)
+#undef SPX_X
+        }
+    }
+};
+
 }  // namespace spx
 
 // Defines the registry entry points of one variant (declared by SPX_DECLARE_VARIANT).
@@ -368,4 +508,5 @@ struct Stockham {
         Stockham<R, TABLE>::columns(x, y, n, cols, slabs, direction, stream);                   \
     }                                                                                           \
     const PrunedFns pruned_##NAME = Stockham<R, TABLE>::pruned_fns();                           \
+    const Fused2dFns fused_##NAME = Fused2dDriver<R, TABLE>::fns();                             \
     }

@@ -144,3 +144,23 @@ def test_rejects_a_spectrum_of_the_wrong_width():
     x = torch.zeros(4, 8, dtype=torch.complex64, device="cuda")
     with pytest.raises(RuntimeError, match="n2/2 \\+ 1 = 5 input columns"):
         spectral.irfft2(x, 8)
+
+
+# Every shape with a single-pass kernel (n1, n2 in 32 .. 256 whose half spectrum fits the LDS
+# tile), with a batch that leaves the last workgroup partly empty (17 = 16 arrays + 1 for 32 x 32).
+FUSED_SHAPES = [(32, 32), (64, 32), (128, 32), (256, 32), (32, 64), (64, 64), (128, 64),
+                (256, 64), (32, 128), (64, 128), (128, 128), (32, 256), (64, 256)]
+FUSED_IMPLS = ["stockham_r4", "stockham_r8", "stockham_r8_table"]
+
+
+@pytest.mark.parametrize("impl", FUSED_IMPLS)
+@pytest.mark.parametrize(("n1", "n2"), FUSED_SHAPES)
+def test_single_pass_rfft2_and_irfft2(rng, impl, n1, n2):
+    x = random_real(rng, (17, n1, n2))
+    y = spectral.rfft2(cuda(x), impl=impl)
+    assert_transform_close(y, ref.rfft2(x), n1 * n2, axes=AXES)
+    two_pass = spectral.rfft2(cuda(x), impl=impl, columns="transpose")
+    assert_transform_close(y, two_pass.cpu().numpy(), n1 * n2, axes=AXES)
+    spectrum = random_complex(rng, (17, n1, n2 // 2 + 1))
+    back = spectral.irfft2(cuda(spectrum), n2, impl=impl)
+    assert_transform_close(back, ref.irfft2(spectrum, (n1, n2)), n1 * n2, axes=AXES)

@@ -161,3 +161,21 @@ def test_rejects_keep_out_of_range():
         spectral.fft_truncated(x, 9)
     with pytest.raises(RuntimeError, match="1 <= keep <= n"):
         spectral.ifft_from_modes(x, 4)
+
+
+# Every shape with a single-pass kernel, with random kept-mode counts and a partial last workgroup.
+FUSED_SHAPES = [(32, 32), (64, 32), (128, 32), (256, 32), (32, 64), (64, 64), (128, 64),
+                (256, 64), (32, 128), (64, 128), (128, 128), (32, 256), (64, 256)]
+
+
+@pytest.mark.parametrize("impl", ["stockham_r4", "stockham_r8", "stockham_r8_table"])
+@pytest.mark.parametrize(("n1", "n2"), FUSED_SHAPES)
+def test_single_pass_modes_round_trip(rng, impl, n1, n2):
+    m1 = int(rng.integers(1, n1 // 2 + 1))
+    m2 = int(rng.integers(1, n2 // 2 + 2))
+    x = random_real(rng, (17, n1, n2))
+    modes = spectral.rfft2_truncated(cuda(x), m1, m2, impl=impl)
+    assert_transform_close(modes, ref.rfft2_truncate(x, m1, m2), n1 * n2, axes=AXES)
+    given = random_complex(rng, (17, 2 * m1, m2))
+    y = spectral.irfft2_from_modes(cuda(given), (n1, n2), impl=impl)
+    assert_transform_close(y, ref.irfft2_from_modes(given, (n1, n2)), n1 * n2, axes=AXES)
