@@ -109,8 +109,14 @@ def test_workspace_queries(lib):
     assert count.value == 2 * 8 * 8 * 2
     assert lib.spx_fft2_r2c_workspace(0, 0, 8, 8, 2, ctypes.byref(count)) == SPX_OK
     assert count.value == 2 * 8 * 5 * 2 + 8 * 4 * 2
+    # 128 x 128 runs as one single-pass kernel (no workspace); 512 x 512 as rows then columns,
+    # through n1 x m2 values per array.
     assert lib.spx_rfft2_modes_workspace(3, 128, 128, 16, 16, 4, ctypes.byref(count)) == SPX_OK
-    assert count.value == 128 * 16 * 4
+    assert count.value == 0
+    assert lib.spx_rfft2_modes_workspace(3, 512, 512, 16, 16, 4, ctypes.byref(count)) == SPX_OK
+    assert count.value == 512 * 16 * 4
+    assert lib.spx_fft2_r2c_workspace(3, 1, 128, 128, 2, ctypes.byref(count)) == SPX_OK
+    assert count.value == 0
     assert lib.spx_fft_c2c_pruned_workspace(0, 64, 8, 3, ctypes.byref(count)) == SPX_OK
     assert count.value == 64 * 3
 
