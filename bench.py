@@ -14,8 +14,9 @@ roofline     the forward C2C kernel alone: the same algorithmic bytes per launch
              from profiles/ when a counter summary for this kernel has been committed.
 cpu_baseline numpy.fft (pocketfft, single thread) on the same kind of complex64 input, forward +
              inverse, on a bounded sample of the workload, in the same GB/s convention.
-extra        secondary rows of the metric: R2C n = 1024 (C2), pruned rfft2 128^2 m = 16 on
-             [64, 32, 128, 128] (C4) in ms, and rocFFT (torch.fft) on the C1 shape.
+extra        secondary rows of the metric, each with rocFFT (torch.fft) on the same shape: C2
+             R2C / C2R at n = 1024, C3 rfft2 / irfft2 at 128^2 x 1024 and 512^2 x 64, C4 pruned
+             rfft2 / irfft2 on [64, 32, 128, 128] with m1 = m2 = 16 (ms and effective GB/s).
 
 Launches rotate over buffer sets totalling well over twice the 256 MB Infinity Cache, so a
 launch cannot read what the previous one left in the cache.
@@ -212,58 +213,76 @@ def main(argv=None) -> int:
 
 
 def secondary_rows(impl: str, dev) -> dict:
-    """R2C n = 1024 (C2), pruned rfft2 on [64, 32, 128, 128] (C4), and rocFFT on the C1 shape."""
+    """The other configurations of the metric, each next to rocFFT (through torch.fft) on the same
+    shape: C2 real transforms at n = 1024, C3 rfft2 / irfft2 at 128^2 x 1024 and 512^2 x 64, C4
+    pruned transforms on [64, 32, 128, 128] with m1 = m2 = 16, and rocFFT on the C1 shape. Inputs
+    rotate over three sets so no call reads what the previous one left in the cache."""
     import torch
 
     import spectral
-    from spectral.benchmark import fft2_modes_work, fft_real_work, time_gpu
+    from spectral.benchmark import (fft2_modes_work, fft2_real_work, fft_real_work, time_gpu)
 
-    out = {}
     g = torch.Generator(device=dev).manual_seed(0)
-    # C2 at n = 1024: 16384 rows, two input sets in rotation.
-    xr = [torch.randn(16384 * 4, 1024, device=dev, generator=g) for _ in range(1)]
-    views = [xr[0][i * 16384:(i + 1) * 16384] for i in range(4)]
-    k = [0]
+    out = {}
 
-    def r2c():
-        k[0] += 1
-        return spectral.rfft(views[k[0] % 4], impl=impl)
+    def timed(fn, inputs):
+        k = [0]
 
-    t = time_gpu(r2c)
-    out["r2c_1024_ms"] = round(t.median_ms, 5)
-    out["r2c_1024_gbps"] = round(fft_real_work(1024, 16384)[1] / (t.median_ms * 1e6), 1)
-    del xr, views
-    # C4: pruned rfft2, [64, 32, 128, 128] -> modes [64, 32, 32, 16].
+        def call():
+            k[0] += 1
+            return fn(inputs[k[0] % len(inputs)])
+
+        return time_gpu(call).median_ms
+
+    def record(name, ms, nbytes, rocfft_ms):
+        out[f"{name}_ms"] = round(ms, 5)
+        out[f"{name}_gbps"] = round(nbytes / (ms * 1e6), 1)
+        out[f"{name}_rocfft_ms"] = round(rocfft_ms, 5)
+
+    # C2: real transforms, n = 1024, 16384 rows.
+    xr = [torch.randn(16384, 1024, device=dev, generator=g) for _ in range(3)]
+    xh = [torch.fft.rfft(x) for x in xr]
+    work = fft_real_work(1024, 16384)[1]
+    record("c2_r2c_1024", timed(lambda x: spectral.rfft(x, impl=impl), xr), work,
+           timed(torch.fft.rfft, xr))
+    record("c2_c2r_1024", timed(lambda x: spectral.irfft(x, 1024, impl=impl), xh), work,
+           timed(lambda x: torch.fft.irfft(x, 1024), xh))
+    del xr, xh
+    # C3: 2D real transforms.
+    for n, arrays in ((128, 1024), (512, 64)):
+        xs = [torch.randn(arrays, n, n, device=dev, generator=g) for _ in range(3)]
+        hs = [torch.fft.rfft2(x) for x in xs]
+        work = fft2_real_work(n, n, arrays)[1]
+        record(f"c3_rfft2_{n}", timed(lambda x: spectral.rfft2(x, impl=impl), xs), work,
+               timed(torch.fft.rfft2, xs))
+        record(f"c3_irfft2_{n}", timed(lambda x: spectral.irfft2(x, n, impl=impl), hs), work,
+               timed(lambda x: torch.fft.irfft2(x, s=(n, n)), hs))
+        del xs, hs
+    # C4: FNO pruned transforms, [64, 32, 128, 128] <-> modes [64, 32, 32, 16].
     xp = [torch.randn(64, 32, 128, 128, device=dev, generator=g) for _ in range(3)]
-    k[0] = 0
+    mp = [spectral.rfft2_truncated(x, 16, 16, impl=impl) for x in xp]
+    work = fft2_modes_work(128, 128, 16, 16, 2048)[1]
 
-    def pruned():
-        k[0] += 1
-        return spectral.rfft2_truncated(xp[k[0] % 3], 16, 16, impl=impl)
-
-    t = time_gpu(pruned)
-    out["pruned_rfft2_128_m16_ms"] = round(t.median_ms, 5)
-    out["pruned_rfft2_128_m16_gbps"] = round(
-        fft2_modes_work(128, 128, 16, 16, 2048)[1] / (t.median_ms * 1e6), 1)
-
-    def rocfft_gather():
-        k[0] += 1
-        full = torch.fft.rfft2(xp[k[0] % 3])
+    def rocfft_gather(x):
+        full = torch.fft.rfft2(x)
         return torch.cat([full[..., :16, :16], full[..., 112:, :16]], dim=-2)
 
-    t = time_gpu(rocfft_gather)
-    out["rocfft_rfft2_128_plus_gather_ms"] = round(t.median_ms, 5)
-    del xp
+    def rocfft_scatter(m):
+        full = torch.zeros(64, 32, 128, 65, dtype=torch.complex64, device=dev)
+        full[..., :16, :16] = m[..., :16, :]
+        full[..., 112:, :16] = m[..., 16:, :]
+        return torch.fft.irfft2(full, s=(128, 128))
+
+    record("c4_rfft2_modes_128_m16",
+           timed(lambda x: spectral.rfft2_truncated(x, 16, 16, impl=impl), xp), work,
+           timed(rocfft_gather, xp))
+    record("c4_irfft2_modes_128_m16",
+           timed(lambda m: spectral.irfft2_from_modes(m, (128, 128), impl=impl), mp), work,
+           timed(rocfft_scatter, mp))
+    del xp, mp
     # rocFFT (through torch.fft) on the C1 shape, forward.
     xc = [torch.randn(BATCH, N, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
-    k[0] = 0
-
-    def roc():
-        k[0] += 1
-        return torch.fft.fft(xc[k[0] % 3])
-
-    t = time_gpu(roc)
-    out["rocfft_c2c_1024_fwd_ms"] = round(t.median_ms, 5)
+    out["c1_rocfft_c2c_1024_fwd_ms"] = round(timed(torch.fft.fft, xc), 5)
     return out
 
 
