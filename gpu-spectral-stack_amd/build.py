@@ -61,6 +61,7 @@ CAPI_SOURCES = [
     "scale.hip",
     "fft2d.hip",
     "pruned.hip",
+    "ns.hip",
     "registry.cpp",
     "capi.cpp",
 ]

@@ -316,3 +316,15 @@ int spx_scatter_modes(const void* modes, void* full, int n1, int w, int m1, int 
 }
 
 }  // extern "C"
+
+int spx_ns_supports(int n) { return spx::ns_supports(n) ? 1 : 0; }
+
+int spx_ns_stage(const void* state, const void* w0, const void* f0, void* out_f, void* out_w,
+                 const void* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
+                 int n, int batch, int stage, hipStream_t stream)
+{
+    return guarded([&] {
+        spx::ns_stage(cc(state), cc(w0), cc(f0), cm(out_f), cm(out_w), cc(forcing_hat), nu,
+                      nu_stride, drag, dt, n, batch, stage, stream);
+    });
+}

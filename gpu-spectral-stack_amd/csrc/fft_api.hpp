@@ -109,6 +109,14 @@ void gather_modes(const cf32* full, cf32* modes, int n1, int w, int m1, int m2, 
 void scatter_modes(const cf32* modes, cf32* full, int n1, int w, int m1, int m2, int batch,
                    hipStream_t stream);
 
+// --- the Navier-Stokes caller (ns.hip): one fused IMEX stage per field ----------------------
+// Modes in the FNO layout with m = n/3 + 1 ((2m) x m per field). stage 0: out_f = F(state),
+// out_w = the predictor; stage 1: out_w = the corrector from w0, f0 and F(state).
+bool ns_supports(int n);
+void ns_stage(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32* out_w,
+              const cf32* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
+              int n, int batch, int stage, hipStream_t stream);
+
 }  // namespace spx
 
 // --- the Stockham variants (stockham_*.hip) ---------------------------------------------------

@@ -1,0 +1,365 @@
+// One pseudo-spectral Navier-Stokes stage per field in one kernel: the whole nonlinear term of the
+// vorticity equation and the IMEX update, for the pruned (FNO) layout, with every intermediate in
+// LDS and registers. This is the MI355X form of the reference's GpuSolver.tendency / step
+// (python/spectral/flow/gpu.py:115-129), which runs one batched inverse transform of four fields,
+// a product, a forward transform and about fifteen elementwise kernels through HBM per tendency.
+//
+// State: omega_hat on the 2/3-rule modes in the layout of rfft2_truncated with m = n/3 + 1 (rows
+// ky = 0 .. m-1 then -m .. -1, columns kx = 0 .. m-1), (2m) x m complex values per field.
+//
+// Per field (one workgroup):
+//   load W = omega_hat (LDS)
+//   pass A: inverse columns of u_hat = i ky psi_hat and wx_hat = i kx omega_hat (psi_hat =
+//           omega_hat / |k|^2) into tiles T1, T2 (n rows x m columns); then per row, the c2r of
+//           both rows and their product u wx, kept in registers
+//   pass B: the same for v_hat = -i kx psi_hat and wy_hat = i ky omega_hat, adding v wy; then per
+//           row the r2c of the product (still in registers), its first m bins into T1
+//   columns: forward transforms of T1's m columns, then the epilogue on the kept rows:
+//           F = f_hat - mask N_hat, and the IMEX update
+//             stage 0: out_f = F, out_w = w* = (e w + dt F) i
+//             stage 1: out_w = w' = (e w + dt/2 (f0 + F)) i
+//           with e = 1 + dt/2 L, i = 1 / (1 - dt/2 L), L = -nu |k|^2 - alpha.
+// Normalization: inverse 1 / n^2 over the column and row passes, forward none, as numpy.
+
+#include "stockham.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace spx {
+namespace dev {
+namespace {
+
+template <int N_>
+struct NsPlan {
+    static constexpr int N = N_;
+    static constexpr int M = N / 2;         // complex values per real row
+    static constexpr int m = N / 3 + 1;      // kept modes per axis
+    static constexpr int rows = 2 * m;       // kept rows
+    static constexpr int TS = m | 1;         // tile row stride (odd: columns hit distinct banks)
+    using PR = Plan<M, 8, default_e<M, 8>()>;   // row transforms (M-point complex)
+    using PC = Plan<N, 8, default_e<N, 8>()>;   // column transforms
+    static constexpr int NT = N >= 128 ? 512 : 256;
+    static constexpr int RPP = NT / PR::L;    // rows per pass
+    static constexpr int kRowPasses = N / RPP;
+    static constexpr int CPP = NT / PC::L;    // columns per pass
+    static constexpr int RS = (pad(M) + 1) | 1;  // scratch row stride
+    // LDS layout, in complex values
+    static constexpr int kW = rows * m;
+    static constexpr int kT = N * TS;
+    static constexpr int kS = RPP * RS;
+    static constexpr int kLds = kW + 2 * kT + kS;
+
+    static_assert(PR::L <= 64 && PC::L <= 64, "wave-local transforms");
+    static_assert(N % RPP == 0, "row passes cover the rows");
+    static_assert(kLds * sizeof(cf32) <= 160 * 1024, "LDS budget");
+};
+
+// Position of output slot (b, r) of the row inverse's last stage in the input slots of the row
+// forward's first stage: both hold the same lane's elements, in different register orders.
+template <class P>
+constexpr int forward_slot_of(int e_out)
+{
+    constexpr int RL = P::template radix<P::kStages - 1>();
+    constexpr int R0 = P::template radix<0>();
+    const int idx = (e_out / RL) * P::L + (e_out % RL) * (P::N / RL);  // lane 0's element
+    for (int e = 0; e < P::E; ++e) {
+        if ((e / R0) * P::L + (e % R0) * (P::N / R0) == idx) {
+            return e;
+        }
+    }
+    return -1;
+}
+
+template <class P>
+constexpr bool slots_match()
+{
+    for (int e = 0; e < P::E; ++e) {
+        if (forward_slot_of<P>(e) < 0) {
+            return false;
+        }
+    }
+    return true;
+}
+
+__device__ __forceinline__ cf32 mul_ik(float k, cf32 z) { return {-k * z.im, k * z.re}; }
+
+// Kept-mode row of full-spectrum row i (0 .. N-1), or -1 when that row is not kept.
+template <class NP>
+__device__ __forceinline__ int mode_row(int i)
+{
+    if (i < NP::m) {
+        return i;
+    }
+    if (i >= NP::N - NP::m) {
+        return i - NP::N + 2 * NP::m;
+    }
+    return -1;
+}
+
+template <class NP>
+__device__ __forceinline__ float ky_of_mode_row(int r)
+{
+    return static_cast<float>(r < NP::m ? r : r - 2 * NP::m);
+}
+
+// The spectrum of derived field `which` at kept mode (r, c) from W (omega_hat):
+//   0: u = i ky psi,  1: wx = i kx omega,  2: v = -i kx psi,  3: wy = i ky omega.
+template <class NP>
+__device__ __forceinline__ cf32 derived(const cf32* W, int r, int c, int which)
+{
+    const cf32 w = W[r * NP::m + c];
+    const float ky = ky_of_mode_row<NP>(r);
+    const float kx = static_cast<float>(c);
+    const float k2 = kx * kx + ky * ky;
+    const float inv_k2 = k2 > 0.0f ? 1.0f / k2 : 0.0f;
+    switch (which) {
+    case 0:
+        return mul_ik(ky, cscale(w, inv_k2));
+    case 1:
+        return mul_ik(kx, w);
+    case 2:
+        return mul_ik(-kx, cscale(w, inv_k2));
+    default:
+        return mul_ik(ky, w);
+    }
+}
+
+// Inverse column transforms of two derived fields (first, first + 1) into T1 and T2.
+template <class NP>
+__device__ __forceinline__ void inverse_columns(const cf32* W, cf32* T1, cf32* T2, int first,
+                                                int tid)
+{
+    using PC = typename NP::PC;
+    constexpr int R0 = PC::template radix<0>();
+    for (int g0 = 0; g0 < 2 * NP::m; g0 += NP::CPP) {
+        const int g = g0 + tid / PC::L;
+        const int lane = tid % PC::L;
+        if (g < 2 * NP::m) {
+            const int f = g / NP::m;
+            const int c = g - f * NP::m;
+            cf32 v[PC::E];
+#pragma unroll
+            for (int b = 0; b < PC::E / R0; ++b) {
+#pragma unroll
+                for (int r = 0; r < R0; ++r) {
+                    const int mr = mode_row<NP>(input_index<PC, 0>(lane, b, r));
+                    v[b * R0 + r] = mr >= 0 ? derived<NP>(W, mr, c, first + f) : czero();
+                }
+            }
+            cf32* const s = (f == 0 ? T1 : T2) + c;
+            run_stages<PC, 0, true, false, Strided<NP::TS>>(v, s, lane, nullptr);
+            lds_sync<true>();
+            final_write<PC, Strided<NP::TS>>(s, v, lane);
+        }
+    }
+}
+
+// Real inverse of tile row `src` (m nonzero bins) for one row: prepare into the scratch row s,
+// M-point inverse transform; on return v holds the row's reals as complex pairs, in the last
+// stage's slots, scaled by `scale`.
+template <class NP>
+__device__ __forceinline__ void row_c2r(const cf32* src, cf32* s, cf32 (&v)[NP::PR::E], int lane,
+                                        float scale)
+{
+    using PR = typename NP::PR;
+    constexpr int M = NP::M;
+    for (int k = lane; k <= M / 2; k += PR::L) {
+        cf32 xk = k < NP::m ? src[k] : czero();
+        cf32 xm = M - k < NP::m ? src[M - k] : czero();
+        if (k == 0) {
+            xk.im = 0.0f;
+            xm.im = 0.0f;
+        }
+        const cf32 ev{0.5f * (xk.re + xm.re), 0.5f * (xk.im - xm.im)};
+        const cf32 d{0.5f * (xk.re - xm.re), 0.5f * (xk.im + xm.im)};
+        const cf32 od = cmul(d, twiddle_of<2 * M, true>(k));
+        const cf32 iod{-od.im, od.re};
+        s[pad(k)] = cadd(ev, iod);
+        if (k > 0 && k < M - k) {
+            s[pad(M - k)] = cconj(csub(ev, iod));
+        }
+    }
+    lds_sync<true>();
+    stage_read<PR, 0>(s, v, lane);
+    run_stages<PR, 0, true, false>(v, s, lane, nullptr);
+#pragma unroll
+    for (int e = 0; e < PR::E; ++e) {
+        v[e] = cscale(v[e], scale);
+    }
+    lds_sync<true>();  // every lane is done with s before it is reused
+}
+
+template <class NP>
+__global__ void __launch_bounds__(NP::NT)
+    ns_stage_kernel(const cf32* __restrict__ state, const cf32* __restrict__ w0,
+                    const cf32* __restrict__ f0, cf32* __restrict__ out_f,
+                    cf32* __restrict__ out_w, const cf32* __restrict__ forcing_hat,
+                    const float* __restrict__ nu, int nu_stride, float drag, float dt, int stage)
+{
+    using PR = typename NP::PR;
+    using PC = typename NP::PC;
+    static_assert(slots_match<PR>(), "row inverse outputs must be the row forward's inputs");
+    __shared__ cf32 lds[NP::kLds];
+    cf32* const W = lds;
+    cf32* const T1 = W + NP::kW;
+    cf32* const T2 = T1 + NP::kT;
+    cf32* const S = T2 + NP::kT;
+
+    const int tid = threadIdx.x;
+    const long long field = blockIdx.x;
+    const long long base = field * NP::kW;
+
+    // Load the state's modes.
+    for (int e = tid; e < NP::kW; e += NP::NT) {
+        W[e] = state[base + e];
+    }
+    __syncthreads();
+
+    constexpr float kInvScale = 1.0f / static_cast<float>(NP::N * NP::M);
+    const int rlane = tid % PR::L;
+    cf32* const s = S + (tid / PR::L) * NP::RS;
+    cf32 nl[NP::kRowPasses][PR::E];
+
+    // Pass A: u and wx, their product per point.
+    inverse_columns<NP>(W, T1, T2, 0, tid);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < NP::kRowPasses; ++p) {
+        const int y = p * NP::RPP + tid / PR::L;
+        cf32 a[PR::E];
+        cf32 b[PR::E];
+        row_c2r<NP>(T1 + y * NP::TS, s, a, rlane, kInvScale);
+        row_c2r<NP>(T2 + y * NP::TS, s, b, rlane, kInvScale);
+#pragma unroll
+        for (int e = 0; e < PR::E; ++e) {
+            nl[p][e] = cf32{a[e].re * b[e].re, a[e].im * b[e].im};
+        }
+    }
+    __syncthreads();
+
+    // Pass B: v and wy; add v wy, then the forward row transform of the product.
+    inverse_columns<NP>(W, T1, T2, 2, tid);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < NP::kRowPasses; ++p) {
+        const int y = p * NP::RPP + tid / PR::L;
+        cf32 a[PR::E];
+        cf32 b[PR::E];
+        row_c2r<NP>(T1 + y * NP::TS, s, a, rlane, kInvScale);
+        row_c2r<NP>(T2 + y * NP::TS, s, b, rlane, kInvScale);
+        cf32 v[PR::E];
+        static_for<0, PR::E>([&](auto ei) {
+            constexpr int e = decltype(ei)::value;
+            constexpr int slot = forward_slot_of<PR>(e);
+            v[slot] = cf32{nl[p][e].re + a[e].re * b[e].re, nl[p][e].im + a[e].im * b[e].im};
+        });
+        run_stages<PR, 0, false, false>(v, s, rlane, nullptr);
+        lds_sync<true>();
+        final_write<PR>(s, v, rlane);
+        lds_sync<true>();
+        constexpr int M = NP::M;
+        for (int k = rlane; k <= M / 2; k += PR::L) {
+            const cf32 zk = s[pad(k & (M - 1))];
+            const cf32 zm = s[pad((M - k) & (M - 1))];
+            const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
+            const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
+            const cf32 wo = cmul(twiddle_of<2 * M, false>(k), od);
+            cf32* const out = T1 + y * NP::TS;
+            if (k < NP::m) {
+                out[k] = cadd(ev, wo);
+            }
+            if (k < M - k && M - k < NP::m) {
+                out[M - k] = cconj(csub(ev, wo));
+            }
+        }
+        lds_sync<true>();
+    }
+    __syncthreads();
+
+    // Forward columns of the product's row spectra, in place in T1.
+    for (int c0 = 0; c0 < NP::m; c0 += NP::CPP) {
+        const int c = c0 + tid / PC::L;
+        const int lane = tid % PC::L;
+        if (c < NP::m) {
+            cf32* const col = T1 + c;
+            cf32 v[PC::E];
+            stage_read<PC, 0, Strided<NP::TS>>(col, v, lane);
+            run_stages<PC, 0, false, false, Strided<NP::TS>>(v, col, lane, nullptr);
+            lds_sync<true>();
+            final_write<PC, Strided<NP::TS>>(col, v, lane);
+        }
+    }
+    __syncthreads();
+
+    // Epilogue on the kept modes.
+    const float nu_f = nu[field * nu_stride];
+    const float kmax = static_cast<float>(NP::N) / 3.0f;
+    for (int e = tid; e < NP::kW; e += NP::NT) {
+        const int r = e / NP::m;
+        const int c = e - r * NP::m;
+        const float ky = ky_of_mode_row<NP>(r);
+        const float kx = static_cast<float>(c);
+        const int i = r < NP::m ? r : r - 2 * NP::m + NP::N;
+        const bool kept = fabsf(kx) <= kmax && fabsf(ky) <= kmax;
+        const cf32 nlh = kept ? T1[i * NP::TS + c] : czero();
+        const cf32 fh = forcing_hat[e];
+        const cf32 F = csub(fh, nlh);
+        const float linear = -nu_f * (kx * kx + ky * ky) - drag;
+        const float ex = 1.0f + 0.5f * dt * linear;
+        const float im = 1.0f / (1.0f - 0.5f * dt * linear);
+        if (stage == 0) {
+            const cf32 w = W[e];
+            out_f[base + e] = F;
+            out_w[base + e] = cscale(cadd(cscale(w, ex), cscale(F, dt)), im);
+        } else {
+            const cf32 w = w0[base + e];
+            const cf32 sum = cadd(f0[base + e], F);
+            out_w[base + e] = cscale(cadd(cscale(w, ex), cscale(sum, 0.5f * dt)), im);
+        }
+    }
+}
+
+template <int N>
+void launch(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32* out_w,
+            const cf32* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
+            int batch, int stage, hipStream_t stream)
+{
+    using NP = NsPlan<N>;
+    hipLaunchKernelGGL(ns_stage_kernel<NP>, dim3(static_cast<unsigned>(batch)), dim3(NP::NT), 0,
+                       stream, state, w0, f0, out_f, out_w, forcing_hat, nu, nu_stride, drag, dt,
+                       stage);
+    SPX_LAUNCH_CHECK();
+}
+
+}  // namespace
+}  // namespace dev
+
+bool ns_supports(int n) { return n == 64 || n == 128; }
+
+void ns_stage(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32* out_w,
+              const cf32* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
+              int n, int batch, int stage, hipStream_t stream)
+{
+    if (!ns_supports(n)) {
+        throw InvalidArgument("ns_stage: the fused Navier-Stokes stage supports n = 64 and 128, "
+                              "got " + str(n));
+    }
+    if (batch < 1 || (stage != 0 && stage != 1) || (nu_stride != 0 && nu_stride != 1)) {
+        throw InvalidArgument("ns_stage: need batch >= 1, stage 0 or 1, nu_stride 0 or 1");
+    }
+    if (stage == 0 && (out_f == nullptr || out_w == nullptr)) {
+        throw InvalidArgument("ns_stage: stage 0 writes both the tendency and the predictor");
+    }
+    if (stage == 1 && (w0 == nullptr || f0 == nullptr || out_w == nullptr)) {
+        throw InvalidArgument("ns_stage: stage 1 reads w and f0 and writes the corrected state");
+    }
+    if (n == 64) {
+        dev::launch<64>(state, w0, f0, out_f, out_w, forcing_hat, nu, nu_stride, drag, dt, batch,
+                        stage, stream);
+    } else {
+        dev::launch<128>(state, w0, f0, out_f, out_w, forcing_hat, nu, nu_stride, drag, dt,
+                         batch, stage, stream);
+    }
+}
+
+}  // namespace spx

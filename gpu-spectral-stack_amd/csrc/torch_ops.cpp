@@ -20,6 +20,7 @@
 #include <climits>
 #include <cstdint>
 #include <string>
+#include <tuple>
 #include <vector>
 
 namespace {
@@ -384,6 +385,78 @@ at::Tensor irfft2_modes_op(const at::Tensor& modes, int64_t n1, int64_t n2,
     return y;
 }
 
+// --- the Navier-Stokes caller: one fused IMEX stage per field (no reference operator; the
+// reference's GpuSolver composes its transforms with torch elementwise ops instead) ----------
+
+void check_ns(const at::Tensor& state, const at::Tensor& forcing_hat, const at::Tensor& nu,
+              int64_t n)
+{
+    check_complex64_cuda(state, "state");
+    check_complex64_cuda(forcing_hat, "forcing_hat");
+    TORCH_CHECK(spx_ns_supports(static_cast<int>(n)) == 1,
+                "ns: the fused Navier-Stokes stage supports n = 64 and 128, got ", n);
+    const int64_t m = n / 3 + 1;
+    TORCH_CHECK(state.dim() >= 2 && state.size(-2) == 2 * m && state.size(-1) == m,
+                "ns: state must hold (..., ", 2 * m, ", ", m, ") modes for n = ", n);
+    TORCH_CHECK(forcing_hat.numel() == 2 * m * m, "ns: forcing_hat must hold ", 2 * m, " x ", m,
+                " modes");
+    TORCH_CHECK(nu.is_cuda() && nu.scalar_type() == at::kFloat,
+                "ns: nu must be a float32 CUDA tensor");
+    const int64_t fields = state.numel() / (2 * m * m);
+    TORCH_CHECK(nu.numel() == 1 || nu.numel() == fields,
+                "ns: nu must hold one viscosity or one per field");
+}
+
+std::tuple<at::Tensor, at::Tensor> ns_predict_op(const at::Tensor& w_hat,
+                                                 const at::Tensor& forcing_hat,
+                                                 const at::Tensor& nu, double drag, double dt,
+                                                 int64_t n)
+{
+    check_ns(w_hat, forcing_hat, nu, n);
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(w_hat.device());
+    const at::Tensor w = w_hat.contiguous();
+    const at::Tensor fh = forcing_hat.contiguous();
+    const at::Tensor nc = nu.contiguous();
+    at::Tensor f0 = at::empty_like(w);
+    at::Tensor predicted = at::empty_like(w);
+    const int64_t m = n / 3 + 1;
+    const int batch = batch_of(w, 2 * m * m, "ns_predict");
+    if (batch > 0) {
+        check_status(spx_ns_stage(cptr(w), nullptr, nullptr, mptr(f0), mptr(predicted),
+                                  cptr(fh), nc.const_data_ptr<float>(), nc.numel() == 1 ? 0 : 1,
+                                  static_cast<float>(drag), static_cast<float>(dt),
+                                  static_cast<int>(n), batch, 0, current_stream()));
+    }
+    return {f0, predicted};
+}
+
+at::Tensor ns_correct_op(const at::Tensor& predicted, const at::Tensor& w_hat,
+                         const at::Tensor& f0, const at::Tensor& forcing_hat,
+                         const at::Tensor& nu, double drag, double dt, int64_t n)
+{
+    check_ns(predicted, forcing_hat, nu, n);
+    TORCH_CHECK(w_hat.sizes() == predicted.sizes() && f0.sizes() == predicted.sizes(),
+                "ns_correct: w_hat, f0 and predicted must have the same shape");
+    check_complex64_cuda(w_hat, "w_hat");
+    check_complex64_cuda(f0, "f0");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(predicted.device());
+    const at::Tensor p = predicted.contiguous();
+    const at::Tensor w = w_hat.contiguous();
+    const at::Tensor f = f0.contiguous();
+    const at::Tensor fh = forcing_hat.contiguous();
+    const at::Tensor nc = nu.contiguous();
+    at::Tensor out = at::empty_like(p);
+    const int64_t m = n / 3 + 1;
+    const int batch = batch_of(p, 2 * m * m, "ns_correct");
+    if (batch > 0) {
+        check_status(spx_ns_stage(cptr(p), cptr(w), cptr(f), nullptr, mptr(out), cptr(fh),
+                                  nc.const_data_ptr<float>(), nc.numel() == 1 ? 0 : 1,
+                                  static_cast<float>(drag), static_cast<float>(dt),
+                                  static_cast<int>(n), batch, 1, current_stream()));
+    }
+    return out;
+}
+
 // spectral._C.fft_impls(): the registry's names, in order, as a tuple of str.
 PyObject* py_fft_impls(PyObject*, PyObject*)
 {
@@ -403,8 +476,20 @@ PyObject* py_fft_impls(PyObject*, PyObject*)
     return names;
 }
 
+// spectral._C.ns_supports(n): whether the fused Navier-Stokes stage has a kernel for an n x n grid.
+PyObject* py_ns_supports(PyObject*, PyObject* arg)
+{
+    const long n = PyLong_AsLong(arg);
+    if (n == -1 && PyErr_Occurred() != nullptr) {
+        return nullptr;
+    }
+    return PyBool_FromLong(n > 0 && n < (1L << 30) && spx_ns_supports(static_cast<int>(n)) == 1);
+}
+
 PyMethodDef module_methods[] = {
     {"fft_impls", py_fft_impls, METH_NOARGS, "Names of the FFT implementations, in order."},
+    {"ns_supports", py_ns_supports, METH_O,
+     "Whether the fused Navier-Stokes stage has a kernel for an n x n grid."},
     {nullptr, nullptr, 0, nullptr},
 };
 
@@ -424,6 +509,11 @@ TORCH_LIBRARY(spectral, m)
           " -> Tensor");
     m.def("rfft2_modes(Tensor x, int m1, int m2, str impl=\"naive\") -> Tensor");
     m.def("irfft2_modes(Tensor modes, int n1, int n2, str impl=\"naive\") -> Tensor");
+    // The Navier-Stokes caller's fused stages (no reference operator).
+    m.def("ns_predict(Tensor w_hat, Tensor forcing_hat, Tensor nu, float drag, float dt, int n)"
+          " -> (Tensor, Tensor)");
+    m.def("ns_correct(Tensor predicted, Tensor w_hat, Tensor f0, Tensor forcing_hat, Tensor nu,"
+          " float drag, float dt, int n) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(spectral, CUDA, m)
@@ -438,6 +528,8 @@ TORCH_LIBRARY_IMPL(spectral, CUDA, m)
     m.impl("fft_c2c_pruned", &fft_c2c_pruned_op);
     m.impl("rfft2_modes", &rfft2_modes_op);
     m.impl("irfft2_modes", &irfft2_modes_op);
+    m.impl("ns_predict", &ns_predict_op);
+    m.impl("ns_correct", &ns_correct_op);
 }
 
 // Importing spectral._C runs the TORCH_LIBRARY blocks (registering torch.ops.spectral) and

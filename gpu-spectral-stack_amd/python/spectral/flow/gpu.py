@@ -18,6 +18,13 @@ masked, so the pruned state equals the full one's kept modes.
 
 fft_impl: one of spectral.FFT_IMPLS (this stack's kernels), or "rocfft" for torch.fft (rocFFT on
 ROCm). "cufft", the reference's name for the torch.fft backend, is accepted as the same thing.
+
+fused (this stack's addition; the reference has no such option): with pruned=True, a Stockham
+fft_impl and n = 64 or 128, each of the step's two stages runs as one kernel per field
+(torch.ops.spectral.ns_predict / ns_correct) that keeps the four derived fields, their product and
+its spectrum in LDS: the same arithmetic as tendency() and the update below, in float32, without
+the intermediate HBM traffic. fused=None picks it whenever it applies; True requires it; False
+turns it off.
 """
 
 from __future__ import annotations
@@ -27,7 +34,7 @@ from collections.abc import Iterator
 import numpy as np
 import torch
 
-from .. import ops
+from .. import _C, ops
 from .params import Flow, Grid, forcing
 
 TORCH_BACKENDS = ("rocfft", "cufft")
@@ -93,10 +100,22 @@ class GpuSolver:
         *,
         fft_impl: str = "stockham_r8",
         pruned: bool = False,
+        fused: bool | None = None,
         device: torch.device | str = "cuda",
     ):
         self.n, self.flow, self.dt = n, flow, dt
         self.spectral = s = Spectral(n, fft_impl, pruned, device)
+        fusable = (
+            pruned
+            and fft_impl.startswith("stockham")
+            and _C.ns_supports(n)
+        )
+        if fused and not fusable:
+            raise ValueError(
+                "fused=True needs pruned=True, a stockham fft_impl and n = 64 or 128 "
+                f"(got pruned={pruned}, fft_impl='{fft_impl}', n={n})"
+            )
+        self.fused = fusable if fused is None else bool(fused)
         self.ikx = (1j * s.kx).to(torch.complex64)
         self.iky = (1j * s.ky).to(torch.complex64)
         k2 = s.kx**2 + s.ky**2
@@ -104,6 +123,7 @@ class GpuSolver:
         f = torch.as_tensor(forcing(Grid(n), flow), dtype=torch.float32, device=device)
         self.forcing_hat = s.forward(f) * s.mask
         nu = torch.as_tensor(np.asarray(flow.viscosity), dtype=torch.float32, device=device)
+        self.nu = nu.reshape(-1).contiguous()  # one value, or one per trajectory
         nu = nu[..., None, None] if nu.dim() else nu
         linear = -nu * k2 - flow.drag
         self.explicit = (1.0 + 0.5 * dt * linear).to(torch.complex64)
@@ -127,6 +147,14 @@ class GpuSolver:
         return self.forcing_hat - nonlinear_hat
 
     def step(self, w_hat: torch.Tensor) -> torch.Tensor:
+        if self.fused:
+            drag, dt, n = float(self.flow.drag), float(self.dt), self.n
+            f0, predicted = torch.ops.spectral.ns_predict.default(
+                w_hat, self.forcing_hat, self.nu, drag, dt, n
+            )
+            return torch.ops.spectral.ns_correct.default(
+                predicted, w_hat, f0, self.forcing_hat, self.nu, drag, dt, n
+            )
         f0 = self.tendency(w_hat)
         predicted = (self.explicit * w_hat + self.dt * f0) * self.implicit
         f1 = self.tendency(predicted)

@@ -133,6 +133,21 @@ int spx_gather_modes(const void* full, void* modes, int n1, int w, int m1, int m
 int spx_scatter_modes(const void* modes, void* full, int n1, int w, int m1, int m2, int batch,
                       hipStream_t stream);
 
+/* --- the Navier-Stokes caller -------------------------------------------------------------
+ * No counterpart in the reference's FFI: its GpuSolver (python/spectral/flow/gpu.py:115-129)
+ * composes the transforms above with torch elementwise kernels. This entry runs one IMEX
+ * Crank-Nicolson / Heun stage of that solver per field as a single kernel, for the pruned
+ * layout with m = n/3 + 1 ((2m) x m complex modes per field, rows ky = 0 .. m-1 then -m .. -1):
+ *   stage 0: out_f = F(state) = f_hat - mask N_hat(state), out_w = (e state + dt F) i
+ *   stage 1: out_w = (e w0 + dt/2 (f0 + F(state))) i
+ * with e = 1 + dt/2 L, i = 1 / (1 - dt/2 L), L = -nu |k|^2 - drag, nu = nu[field * nu_stride]
+ * (nu_stride 0: one viscosity for all fields). forcing_hat: (2m) x m modes shared by all fields.
+ * spx_ns_supports(n) is 1 for the grid sizes with a kernel (64, 128). */
+int spx_ns_supports(int n);
+int spx_ns_stage(const void* state, const void* w0, const void* f0, void* out_f, void* out_w,
+                 const void* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
+                 int n, int batch, int stage, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

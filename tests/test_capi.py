@@ -101,6 +101,26 @@ def test_argument_errors_come_back_as_einval(lib):
     assert "no pruned kernels" in _last(lib)
 
 
+def test_navier_stokes_stage_arguments(lib):
+    assert [lib.spx_ns_supports(n) for n in (32, 64, 128, 256)] == [0, 1, 1, 0]
+    p = ctypes.c_void_p(0x1000)
+    f = ctypes.c_float
+    assert lib.spx_ns_stage(p, None, None, p, p, p, p, 0, f(0.1), f(1e-3), 32, 1, 0,
+                            None) == SPX_EINVAL
+    assert "supports n = 64 and 128" in _last(lib)
+    assert lib.spx_ns_stage(p, None, None, p, p, p, p, 0, f(0.1), f(1e-3), 64, 1, 2,
+                            None) == SPX_EINVAL
+    assert "stage 0 or 1" in _last(lib)
+    assert lib.spx_ns_stage(p, None, None, p, p, p, p, 0, f(0.1), f(1e-3), 64, 0, 0,
+                            None) == SPX_EINVAL
+    assert lib.spx_ns_stage(p, None, None, None, p, p, p, 0, f(0.1), f(1e-3), 64, 1, 0,
+                            None) == SPX_EINVAL
+    assert "writes both" in _last(lib)
+    assert lib.spx_ns_stage(p, None, None, None, p, p, p, 0, f(0.1), f(1e-3), 64, 1, 1,
+                            None) == SPX_EINVAL
+    assert "stage 1 reads" in _last(lib)
+
+
 def test_workspace_queries(lib):
     count = ctypes.c_size_t()
     assert lib.spx_fft2_c2c_workspace(3, 1, 8, 8, 2, ctypes.byref(count)) == SPX_OK

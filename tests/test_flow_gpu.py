@@ -23,8 +23,10 @@ CONFIGS = [
 IDS = [f"{impl}-{'pruned' if pruned else 'full'}" for impl, pruned in CONFIGS]
 
 
-def run(w0, flow, dt, steps, impl, pruned, record_every=None):
-    solver = GpuSolver(w0.shape[-1], flow, dt, fft_impl=impl, pruned=pruned)
+def run(w0, flow, dt, steps, impl, pruned, record_every=None, fused=False):
+    # fused=False: these tests cover the composed path (transforms + torch elementwise ops) at
+    # every size; the fused single-kernel stages have their own tests in test_flow_fused.py.
+    solver = GpuSolver(w0.shape[-1], flow, dt, fft_impl=impl, pruned=pruned, fused=fused)
     w = torch.as_tensor(w0, dtype=torch.float32, device="cuda")
     out = solver.simulate(w, steps, record_every or max(steps, 1))
     return out.double().cpu().numpy()
