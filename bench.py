@@ -16,7 +16,10 @@ cpu_baseline numpy.fft (pocketfft, single thread) on the same kind of complex64 
              inverse, on a bounded sample of the workload, in the same GB/s convention.
 extra        secondary rows of the metric, each with rocFFT (torch.fft) on the same shape: C2
              R2C / C2R at n = 1024, C3 rfft2 / irfft2 at 128^2 x 1024 and 512^2 x 64, C4 pruned
-             rfft2 / irfft2 on [64, 32, 128, 128] with m1 = m2 = 16 (ms and effective GB/s).
+             rfft2 / irfft2 on [64, 32, 128, 128] with m1 = m2 = 16 (ms and effective GB/s);
+             C5 the Navier-Stokes solver on 128^2 x 256 trajectories, 32 frames 40 steps apart,
+             fused (this stack's default for the pruned layout) next to this stack's composed
+             pruned path, rocFFT pruned and rocFFT full (ms per step and trajectory-steps / s).
 
 Launches rotate over buffer sets totalling well over twice the 256 MB Infinity Cache, so a
 launch cannot read what the previous one left in the cache.
@@ -181,6 +184,7 @@ def main(argv=None) -> int:
              "fwd_gbps": round(achieved, 1), "wall_s_timed": round(wall_s, 3)}
     if not args.no_extra:
         extra.update(secondary_rows(args.impl, dev))
+        extra.update(navier_stokes_rows(args.impl, dev))
 
     line = {
         "metric": "effective HBM GB/s (% of peak) batched fp32 C2C/R2C at 2^24 points; "
@@ -283,6 +287,65 @@ def secondary_rows(impl: str, dev) -> dict:
     # rocFFT (through torch.fft) on the C1 shape, forward.
     xc = [torch.randn(BATCH, N, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
     out["c1_rocfft_c2c_1024_fwd_ms"] = round(timed(torch.fft.fft, xc), 5)
+    return out
+
+
+def random_vorticity(rng, n: int, batch: int, slope: float = -3.0):
+    """Gaussian random vorticity fields with power spectrum |k|^slope, zero mean, unit RMS."""
+    import numpy as np
+
+    kx = np.fft.rfftfreq(n, 1.0 / n)[None, :]
+    ky = np.fft.fftfreq(n, 1.0 / n)[:, None]
+    k = np.sqrt(kx**2 + ky**2)
+    amplitude = np.where(k > 0, k, 1.0) ** (slope / 2) * (k > 0)
+    w = np.fft.irfft2(np.fft.rfft2(rng.standard_normal((batch, n, n))) * amplitude, s=(n, n))
+    return (w / w.std(axis=(-2, -1), keepdims=True)).astype(np.float32)
+
+
+def navier_stokes_rows(impl: str, dev) -> dict:
+    """C5: the pseudo-spectral Navier-Stokes solver (spectral.flow.gpu.GpuSolver) on 128^2 x 256
+    trajectories, viscosity U[1e-3, 5e-3] per trajectory, Kolmogorov forcing sin(4y), dt 0.0025,
+    a k^-3 Gaussian random initial vorticity from seed 0; one job = 32 physical frames 40 steps
+    apart (1240 IMEX steps, frames kept on the GPU). Timed once per backend after 40 warm-up
+    steps: the fused stages (impl, pruned), this stack's composed pruned path, rocFFT pruned and
+    rocFFT full (the reference's torch.fft comparison)."""
+    import numpy as np
+    import torch
+
+    from spectral.flow import Flow
+    from spectral.flow.gpu import GpuSolver
+
+    n, batch, dt, frames, every = 128, 256, 0.0025, 32, 40
+    rng = np.random.default_rng(0)
+    flow = Flow(viscosity=rng.uniform(1e-3, 5e-3, batch))
+    w0 = torch.as_tensor(random_vorticity(rng, n, batch), device=dev)
+    out = {}
+    record = torch.empty(frames, batch, n, n, device=dev)
+    for name, kwargs in (("fused", dict(fft_impl=impl, pruned=True, fused=True)),
+                         ("composed", dict(fft_impl=impl, pruned=True, fused=False)),
+                         ("rocfft_pruned", dict(fft_impl="rocfft", pruned=True)),
+                         ("rocfft_full", dict(fft_impl="rocfft", pruned=False))):
+        solver = GpuSolver(n, flow, dt, device=dev, **kwargs)
+        w_hat = solver.to_spectral(w0)
+        for _ in range(every):
+            w_hat = solver.step(w_hat)
+        w_hat = solver.to_spectral(w0)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        record[0] = solver.to_physical(w_hat)
+        for f in range(1, frames):
+            for _ in range(every):
+                w_hat = solver.step(w_hat)
+            record[f] = solver.to_physical(w_hat)
+        stop.record()
+        stop.synchronize()
+        seconds = start.elapsed_time(stop) / 1e3
+        steps = (frames - 1) * every
+        if not bool(torch.isfinite(record[-1]).all()):
+            raise RuntimeError(f"C5 {name}: the solution is not finite")
+        out[f"c5_ns128_{name}_ms_per_step"] = round(1e3 * seconds / steps, 5)
+        out[f"c5_ns128_{name}_traj_steps_per_s"] = round(batch * steps / seconds)
     return out
 
 
