@@ -14,6 +14,9 @@ namespace spx {
 
 constexpr int kStockhamMaxN = 4096;                          // one kernel, LDS-resident
 constexpr int kFourStepMaxN = kStockhamMaxN * kStockhamMaxN;  // 2^24 (reference fft.hpp:18-21)
+// C2C sizes above kStockhamMaxN that still run as one kernel per transform (the whole transform
+// in one workgroup's LDS); the four-step split takes over beyond.
+constexpr int kSinglePassMaxN = 16384;
 
 // reference fft.hpp:14-15, 36-39, 59-60
 using C2cFn = void (*)(const cf32* x, cf32* y, int n, int batch, Direction direction,

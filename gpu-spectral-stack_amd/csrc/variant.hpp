@@ -96,6 +96,26 @@ void dispatch_columns(int n, const Io& io, long long batch, hipStream_t stream)
     }
 }
 
+// Single-pass transforms beyond 4096 points: one transform per workgroup of 1024 lanes (N / 1024
+// values per lane), the whole transform in LDS between stages (69,640 B at 8192 points, two
+// workgroups per CU; 139,272 B at 16384, one). Measured on MI355X at 2^24 points: 8192 ran at
+// 62-64 % of the 8 TB/s peak for radix 4 and 8 with 1024 lanes (512 or 256 lanes: 58-61 %);
+// 16384 at 50 % (radix 8) and 53 % (radix 16), where the four-step split took 8 % and 13 %.
+template <int N, int R>
+using LargePlan = Plan<N, (N == 16384 && R == 8) ? 16 : R, N / kMaxBlock, kMaxBlock>;
+
+template <int R, bool Inv, bool Table, class Io>
+void dispatch_large(int n, const Io& io, long long batch, hipStream_t stream)
+{
+    if (n == 8192) {
+        launch<LargePlan<8192, R>, Inv, Table>(io, batch, stream);
+    } else if (n == 16384) {
+        launch<LargePlan<16384, R>, Inv, Table>(io, batch, stream);
+    } else {
+        throw InvalidArgument("stockham: unsupported size " + str(n));
+    }
+}
+
 template <int R, bool Table, class Io>
 void dispatch_dir(int n, bool inverse, const Io& io, long long batch, hipStream_t stream)
 {
@@ -226,7 +246,7 @@ struct Stockham {
         }
     }
 
-    // Any power of two up to kFourStepMaxN: one kernel up to 4096, four steps beyond.
+    // Any power of two up to kFourStepMaxN: one kernel up to kSinglePassMaxN, four steps beyond.
     static void c2c(const cf32* x, cf32* y, int n, int batch, Direction direction,
                     hipStream_t stream)
     {
@@ -244,6 +264,16 @@ struct Stockham {
         const std::size_t total = static_cast<std::size_t>(n) * static_cast<std::size_t>(batch);
         if (x < y + total && y < x + total) {
             throw InvalidArgument("fourstep: x and y must not overlap (out-of-place only)");
+        }
+        if (n <= kSinglePassMaxN) {
+            const bool inverse = direction == Direction::Inverse;
+            const dev::C2cIo<false> io{x, y, inverse ? 1.0f / static_cast<float>(n) : 1.0f, n, n};
+            if (inverse) {
+                dev::dispatch_large<R, true, Table>(n, io, batch, stream);
+            } else {
+                dev::dispatch_large<R, false, Table>(n, io, batch, stream);
+            }
+            return;
         }
         constexpr int n2 = kStockhamMaxN;
         const int n1 = n / n2;

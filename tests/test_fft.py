@@ -21,7 +21,8 @@ pytestmark = pytest.mark.gpu
 IMPLS = spectral.FFT_IMPLS
 SIZES = [1, *POW2_SIZES]
 STOCKHAM = [impl for impl in IMPLS if impl.startswith("stockham")]
-LARGE_SIZES = [8192, 1 << 16, 1 << 20]
+# 8192 and 16384 run as one kernel per transform (a workgroup's LDS holds it); beyond, four-step.
+LARGE_SIZES = [8192, 16384, 32768, 1 << 16, 1 << 20]
 
 
 def run(x: np.ndarray, *, inverse: bool = False, impl: str) -> np.ndarray:
@@ -76,6 +77,16 @@ def test_large_inverse_matches_the_oracle(rng, impl, n, batch):
     assert_transform_close(run(x, inverse=True, impl=impl), ref.ifft(x), n)
 
 
+@pytest.mark.parametrize("impl", STOCKHAM)
+@pytest.mark.parametrize(("n", "batch"), [(8192, 513), (16384, 300)])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_single_pass_large_sizes_over_many_workgroups(rng, impl, n, batch, inverse):
+    # More transforms than CUs: every workgroup of 1024 lanes owns one whole transform.
+    x = random_complex(rng, (batch, n))
+    expected = ref.ifft(x) if inverse else ref.fft(x)
+    assert_transform_close(run(x, inverse=inverse, impl=impl), expected, n)
+
+
 @pytest.mark.parametrize("impl", IMPLS)
 def test_largest_size(rng, impl):
     n = 1 << 24  # 4096 x 4096 in the four-step split
@@ -84,8 +95,9 @@ def test_largest_size(rng, impl):
 
 
 @pytest.mark.parametrize("impl", IMPLS)
-def test_large_single_frequency_lands_in_one_bin(impl):
-    n, k0 = 1 << 20, 12345
+@pytest.mark.parametrize("n", [16384, 1 << 20])
+def test_large_single_frequency_lands_in_one_bin(impl, n):
+    k0 = 12345
     m = np.arange(n)
     x = np.exp(2j * np.pi * k0 * m / n).astype(np.complex64)[None, :]
     expected = np.zeros((1, n), dtype=np.complex128)
