@@ -19,7 +19,10 @@ extra        secondary rows of the metric, each with rocFFT (torch.fft) on the s
              rfft2 / irfft2 on [64, 32, 128, 128] with m1 = m2 = 16 (ms and effective GB/s);
              C5 the Navier-Stokes solver on 128^2 x 256 trajectories, 32 frames 40 steps apart,
              fused (this stack's default for the pruned layout) next to this stack's composed
-             pruned path, rocFFT pruned and rocFFT full (ms per step and trajectory-steps / s).
+             pruned path, rocFFT pruned and rocFFT full (ms per step and trajectory-steps / s);
+             the radio callers (spectral.rf) on 2^22 samples as the reference's bench_rf.py
+             times them: FIR of 63 and 1025 taps and the Hann spectrum of 1024-sample frames,
+             this stack's single kernels next to the same operations on torch.fft.
 
 Launches rotate over buffer sets totalling well over twice the 256 MB Infinity Cache, so a
 launch cannot read what the previous one left in the cache.
@@ -185,6 +188,7 @@ def main(argv=None) -> int:
     if not args.no_extra:
         extra.update(secondary_rows(args.impl, dev))
         extra.update(navier_stokes_rows(args.impl, dev))
+        extra.update(radio_rows(args.impl, dev))
 
     line = {
         "metric": "effective HBM GB/s (% of peak) batched fp32 C2C/R2C at 2^24 points; "
@@ -287,6 +291,37 @@ def secondary_rows(impl: str, dev) -> dict:
     # rocFFT (through torch.fft) on the C1 shape, forward.
     xc = [torch.randn(BATCH, N, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
     out["c1_rocfft_c2c_1024_fwd_ms"] = round(timed(torch.fft.fft, xc), 5)
+    return out
+
+
+def radio_rows(impl: str, dev) -> dict:
+    """spectral.rf as the reference's bench/bench_rf.py times it: 2^22 complex64 samples from
+    seed 0, FIR of 63 and 1025 random taps (default block sizes 256 and 4096), and the Hann
+    spectrum of 1024-sample frames; effective GB/s counts 16 bytes per sample (each read and
+    written once)."""
+    import torch
+
+    from spectral import rf
+    from spectral.benchmark import time_gpu
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    n = 1 << 22
+    x = torch.randn(n, dtype=torch.complex64, device=dev, generator=g)
+    out = {}
+
+    def record(name, fn_ours, fn_torch):
+        ms = time_gpu(fn_ours).median_ms
+        out[f"{name}_ms"] = round(ms, 5)
+        out[f"{name}_gbps"] = round(16.0 * n / (ms * 1e6), 1)
+        out[f"{name}_rocfft_ms"] = round(time_gpu(fn_torch).median_ms, 5)
+
+    for m in (63, 1025):
+        taps = torch.randn(m, device=dev, generator=g)
+        record(f"rf_fir{m}_2e22", lambda t=taps: rf.fir(x, t, fft_impl=impl),
+               lambda t=taps: rf.fir(x, t, fft_impl="rocfft"))
+    record("rf_spectrum1024_hann_2e22",
+           lambda: rf.spectrum(x, 1024, window_name="hann", fft_impl=impl),
+           lambda: rf.spectrum(x, 1024, window_name="hann", fft_impl="rocfft"))
     return out
 
 

@@ -77,6 +77,14 @@ const spx::PrunedFns& pruned_of(const spx::FftImpl& impl)
     return *impl.pruned;
 }
 
+const spx::RfFns& rf_of(const spx::FftImpl& impl)
+{
+    if (impl.rf == nullptr) {
+        throw spx::InvalidArgument(std::string(impl.name) + " has no fused radio kernels");
+    }
+    return *impl.rf;
+}
+
 std::string join_names()
 {
     std::string names;
@@ -315,7 +323,6 @@ int spx_scatter_modes(const void* modes, void* full, int n1, int w, int m1, int 
         [&] { spx::scatter_modes(cc(modes), cm(full), n1, w, m1, m2, batch, stream); });
 }
 
-}  // extern "C"
 
 int spx_ns_supports(int n) { return spx::ns_supports(n) ? 1 : 0; }
 
@@ -328,3 +335,27 @@ int spx_ns_stage(const void* state, const void* w0, const void* f0, void* out_f,
                       nu_stride, drag, dt, n, batch, stage, stream);
     });
 }
+
+int spx_rf_max_nfft(int impl)
+{
+    if (impl < 0 || impl >= spx::impl_count() || spx::impls()[impl].rf == nullptr) {
+        return 0;
+    }
+    return spx::impls()[impl].rf->max_nfft;
+}
+
+int spx_rf_spectrum(int impl, const void* x, const float* window, void* y, long long n,
+                    int nfft, long long rows, hipStream_t stream)
+{
+    return guarded([&] { rf_of(impl_at(impl)).spectrum(cc(x), window, cm(y), n, nfft, rows, stream); });
+}
+
+int spx_rf_fir(int impl, const void* x, const void* h, void* y, long long n, int taps, int nfft,
+               long long rows, hipStream_t stream)
+{
+    return guarded([&] {
+        rf_of(impl_at(impl)).fir(cc(x), cc(h), cm(y), n, taps, nfft, rows, stream);
+    });
+}
+
+}  // extern "C"

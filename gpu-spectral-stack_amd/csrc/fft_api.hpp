@@ -50,6 +50,18 @@ struct Fused2dFns {
                 hipStream_t stream);
 };
 
+// The radio callers (rf.hpp): windowed spectrum of back-to-back frames, and overlap-save FIR.
+// Rows of n complex samples; nfft a power of two from 2 to max_nfft.
+struct RfFns {
+    // y (rows, ceil(n / nfft) or 1, nfft) = FFT of each frame of x times window (nullptr: rect).
+    void (*spectrum)(const cf32* x, const float* window, cf32* y, long long n, int nfft,
+                     long long rows, hipStream_t stream);
+    // y (rows, n) = x filtered by the taps whose nfft-point spectrum is h (taps <= nfft).
+    void (*fir)(const cf32* x, const cf32* h, cf32* y, long long n, int taps, int nfft,
+                long long rows, hipStream_t stream);
+    int max_nfft;
+};
+
 // One implementation, by name (reference registry.hpp:14-25).
 struct FftImpl {
     const char* name;
@@ -63,6 +75,7 @@ struct FftImpl {
     int max_real_n;           // largest real transform
     bool real_needs_work;     // r2c and c2r use the work buffer
     const Fused2dFns* fused;  // single-pass 2D kernels, or nullptr
+    const RfFns* rf;          // the radio callers' fused kernels, or nullptr
 };
 
 // The registry, in the reference's order (registry.hpp:28-40).
@@ -131,7 +144,8 @@ void ns_stage(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf
     void columns_##NAME(const cf32* x, cf32* y, int n, int cols, int slabs,                    \
                         Direction direction, hipStream_t stream);                               \
     extern const PrunedFns pruned_##NAME;                                                      \
-    extern const Fused2dFns fused_##NAME;
+    extern const Fused2dFns fused_##NAME;                                                      \
+    extern const RfFns rf_##NAME;
 
 namespace spx {
 SPX_DECLARE_VARIANT(stockham_r2)

@@ -54,33 +54,6 @@ struct NsPlan {
     static_assert(kLds * sizeof(cf32) <= 160 * 1024, "LDS budget");
 };
 
-// Position of output slot (b, r) of the row inverse's last stage in the input slots of the row
-// forward's first stage: both hold the same lane's elements, in different register orders.
-template <class P>
-constexpr int forward_slot_of(int e_out)
-{
-    constexpr int RL = P::template radix<P::kStages - 1>();
-    constexpr int R0 = P::template radix<0>();
-    const int idx = (e_out / RL) * P::L + (e_out % RL) * (P::N / RL);  // lane 0's element
-    for (int e = 0; e < P::E; ++e) {
-        if ((e / R0) * P::L + (e % R0) * (P::N / R0) == idx) {
-            return e;
-        }
-    }
-    return -1;
-}
-
-template <class P>
-constexpr bool slots_match()
-{
-    for (int e = 0; e < P::E; ++e) {
-        if (forward_slot_of<P>(e) < 0) {
-            return false;
-        }
-    }
-    return true;
-}
-
 __device__ __forceinline__ cf32 mul_ik(float k, cf32 z) { return {-k * z.im, k * z.re}; }
 
 // Kept-mode row of full-spectrum row i (0 .. N-1), or -1 when that row is not kept.

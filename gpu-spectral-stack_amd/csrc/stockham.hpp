@@ -555,6 +555,35 @@ __device__ __forceinline__ void run_stages(cf32 (&v)[P::E], cf32* s, int lane, c
     }
 }
 
+// Slot of the first stage's inputs that holds the element the last stage leaves in slot e_out.
+// Both hold the same elements of a lane, lane + q L for q < E (b L + r N / R covers every q
+// once at any radix), in different register orders: a transform's output can feed another
+// transform's first stage (an inverse after a forward, on the same lanes) by renaming registers.
+template <class P>
+constexpr int forward_slot_of(int e_out)
+{
+    constexpr int RL = P::template radix<P::kStages - 1>();
+    constexpr int R0 = P::template radix<0>();
+    const int idx = (e_out / RL) * P::L + (e_out % RL) * (P::N / RL);  // lane 0's element
+    for (int e = 0; e < P::E; ++e) {
+        if ((e / R0) * P::L + (e % R0) * (P::N / R0) == idx) {
+            return e;
+        }
+    }
+    return -1;
+}
+
+template <class P>
+constexpr bool slots_match()
+{
+    for (int e = 0; e < P::E; ++e) {
+        if (forward_slot_of<P>(e) < 0) {
+            return false;
+        }
+    }
+    return true;
+}
+
 // Writes the last stage's outputs to LDS in natural order (for a staged store).
 template <class P, class Lay = Padded>
 __device__ __forceinline__ void final_write(cf32* s, const cf32 (&v)[P::E], int lane)

@@ -19,6 +19,7 @@
 
 #include <climits>
 #include <cstdint>
+#include <optional>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -385,6 +386,68 @@ at::Tensor irfft2_modes_op(const at::Tensor& modes, int64_t n1, int64_t n2,
     return y;
 }
 
+// --- the radio callers: windowed framed spectrum and overlap-save FIR, one kernel each (no
+// reference operator; the reference's rf.py composes fft_c2c with torch ops) ----------------
+
+at::Tensor rf_spectrum_op(const at::Tensor& x, const std::optional<at::Tensor>& window,
+                          int64_t nfft, c10::string_view impl_name)
+{
+    check_complex64_cuda(x, "x");
+    TORCH_CHECK(x.dim() >= 1, "rf_spectrum: x needs at least one dimension");
+    const Impl impl = find_impl(impl_name);
+    TORCH_CHECK_VALUE(spx_rf_max_nfft(impl.index) > 0, impl.info.name,
+                      " has no fused radio kernels");
+    TORCH_CHECK_VALUE(nfft >= 2 && nfft <= spx_rf_max_nfft(impl.index) && (nfft & (nfft - 1)) == 0,
+                      "rf_spectrum: nfft must be a power of two from 2 to ",
+                      spx_rf_max_nfft(impl.index), ", got ", nfft);
+    const int64_t n = x.size(-1);
+    const int64_t frames = n > nfft ? (n + nfft - 1) / nfft : 1;
+    std::vector<int64_t> shape = x.sizes().vec();
+    shape.back() = frames;
+    shape.push_back(nfft);
+    at::Tensor y = at::empty(shape, x.options());
+    const int64_t rows = n > 0 ? x.numel() / n : (x.numel() == 0 ? y.numel() / (frames * nfft) : 0);
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    const at::Tensor xc = x.contiguous();
+    at::Tensor w;
+    const float* wp = nullptr;
+    if (window.has_value()) {
+        w = window->contiguous();
+        TORCH_CHECK(w.is_cuda() && w.scalar_type() == at::kFloat && w.numel() == nfft,
+                    "rf_spectrum: window must be a float32 CUDA tensor of nfft values");
+        wp = w.const_data_ptr<float>();
+    }
+    if (y.numel() > 0) {
+        check_status(spx_rf_spectrum(impl.index, n > 0 ? cptr(xc) : nullptr, wp, mptr(y), n,
+                                     static_cast<int>(nfft), rows, current_stream()));
+    }
+    return y;
+}
+
+at::Tensor rf_fir_op(const at::Tensor& x, const at::Tensor& h, int64_t taps, int64_t nfft,
+                     c10::string_view impl_name)
+{
+    check_complex64_cuda(x, "x");
+    check_complex64_cuda(h, "h");
+    TORCH_CHECK(x.dim() >= 1, "rf_fir: x needs at least one dimension");
+    const Impl impl = find_impl(impl_name);
+    TORCH_CHECK_VALUE(spx_rf_max_nfft(impl.index) > 0, impl.info.name,
+                      " has no fused radio kernels");
+    TORCH_CHECK_VALUE(h.numel() == nfft, "rf_fir: h must hold the nfft = ", nfft,
+                      " point spectrum of the taps");
+    at::Tensor y = at::empty(x.sizes(), x.options());
+    const int64_t n = x.size(-1);
+    if (x.numel() == 0) {
+        return y;
+    }
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    const at::Tensor xc = x.contiguous();
+    const at::Tensor hc = h.contiguous();
+    check_status(spx_rf_fir(impl.index, cptr(xc), cptr(hc), mptr(y), n, static_cast<int>(taps),
+                            static_cast<int>(nfft), x.numel() / n, current_stream()));
+    return y;
+}
+
 // --- the Navier-Stokes caller: one fused IMEX stage per field (no reference operator; the
 // reference's GpuSolver composes its transforms with torch elementwise ops instead) ----------
 
@@ -509,6 +572,9 @@ TORCH_LIBRARY(spectral, m)
           " -> Tensor");
     m.def("rfft2_modes(Tensor x, int m1, int m2, str impl=\"naive\") -> Tensor");
     m.def("irfft2_modes(Tensor modes, int n1, int n2, str impl=\"naive\") -> Tensor");
+    // The radio callers' fused kernels (no reference operator).
+    m.def("rf_spectrum(Tensor x, Tensor? window, int nfft, str impl) -> Tensor");
+    m.def("rf_fir(Tensor x, Tensor h, int taps, int nfft, str impl) -> Tensor");
     // The Navier-Stokes caller's fused stages (no reference operator).
     m.def("ns_predict(Tensor w_hat, Tensor forcing_hat, Tensor nu, float drag, float dt, int n)"
           " -> (Tensor, Tensor)");
@@ -528,6 +594,8 @@ TORCH_LIBRARY_IMPL(spectral, CUDA, m)
     m.impl("fft_c2c_pruned", &fft_c2c_pruned_op);
     m.impl("rfft2_modes", &rfft2_modes_op);
     m.impl("irfft2_modes", &irfft2_modes_op);
+    m.impl("rf_spectrum", &rf_spectrum_op);
+    m.impl("rf_fir", &rf_fir_op);
     m.impl("ns_predict", &ns_predict_op);
     m.impl("ns_correct", &ns_correct_op);
 }

@@ -9,9 +9,11 @@
 
 #include "fft2_fused.hpp"
 #include "fft_api.hpp"
+#include "rf.hpp"
 #include "stockham.hpp"
 
 #include <climits>
+#include <type_traits>
 
 namespace spx {
 
@@ -514,6 +516,90 @@ struct Fused2dDriver {
     }
 };
 
+// The radio callers' kernels of one variant (rf.hpp): the plans of dispatch and dispatch_large.
+template <int R, bool Table>
+struct RfDriver {
+    template <int N>
+    using PlanOf = std::conditional_t<(N > kStockhamMaxN), dev::LargePlan<N, R>,
+                                      dev::Plan<N, R, dev::default_e<N, R>()>>;
+
+    static void check(long long n, int nfft, long long rows, const char* who)
+    {
+        if (!is_pow2(nfft) || nfft < 2 || nfft > kSinglePassMaxN) {
+            throw InvalidArgument(std::string(who) + ": nfft must be a power of two from 2 to "
+                                  + str(kSinglePassMaxN) + ", got " + str(nfft));
+        }
+        if (n < 0 || rows < 0) {
+            throw InvalidArgument(std::string(who) + ": n and rows must not be negative");
+        }
+    }
+
+    template <class F>
+    static void by_size(int nfft, F&& f)
+    {
+        switch (nfft) {
+#define SPX_CASE(N)                                     \
+    case N:                                             \
+        f(std::integral_constant<int, N>{});            \
+        break;
+            SPX_CASE(2)
+            SPX_CASE(4)
+            SPX_CASE(8)
+            SPX_CASE(16)
+            SPX_CASE(32)
+            SPX_CASE(64)
+            SPX_CASE(128)
+            SPX_CASE(256)
+            SPX_CASE(512)
+            SPX_CASE(1024)
+            SPX_CASE(2048)
+            SPX_CASE(4096)
+            SPX_CASE(8192)
+            SPX_CASE(16384)
+#undef SPX_CASE
+        default:
+            throw InvalidArgument("rf: unsupported nfft " + str(nfft));
+        }
+    }
+
+    static void spectrum(const cf32* x, const float* window, cf32* y, long long n, int nfft,
+                         long long rows, hipStream_t stream)
+    {
+        check(n, nfft, rows, "spectrum");
+        const long long frames = n > nfft ? (n + nfft - 1) / nfft : 1;
+        const long long transforms = rows * frames;
+        if (transforms == 0) {
+            return;
+        }
+        const dev::FramesIo io{x, window, y, n, frames};
+        by_size(nfft, [&](auto size) {
+            dev::launch<PlanOf<decltype(size)::value>, false, Table>(io, transforms, stream);
+        });
+    }
+
+    static void fir(const cf32* x, const cf32* h, cf32* y, long long n, int taps, int nfft,
+                    long long rows, hipStream_t stream)
+    {
+        check(n, nfft, rows, "fir");
+        if (taps < 1 || taps > nfft) {
+            throw InvalidArgument("fir: nfft must be a power of two of at least len(taps) = "
+                                  + str(taps) + ", got " + str(nfft));
+        }
+        const int step = nfft - taps + 1;
+        const long long blocks = n > step ? (n + step - 1) / step : 1;
+        if (rows == 0 || n == 0) {
+            return;
+        }
+        const cf32* table = Table ? twiddle_table() : nullptr;
+        by_size(nfft, [&](auto size) {
+            dev::launch_fir<PlanOf<decltype(size)::value>, Table>(x, h, y, n, taps, step, blocks,
+                                                                  rows * blocks, table, stream);
+        });
+    }
+
+    static RfFns fns() { return {&spectrum, &fir, kSinglePassMaxN}; }
+};
+
 }  // namespace spx
 
 // Defines the registry entry points of one variant (declared by SPX_DECLARE_VARIANT).
@@ -539,4 +625,5 @@ struct Fused2dDriver {
     }                                                                                           \
     const PrunedFns pruned_##NAME = Stockham<R, TABLE>::pruned_fns();                           \
     const Fused2dFns fused_##NAME = Fused2dDriver<R, TABLE>::fns();                             \
+    const RfFns rf_##NAME = RfDriver<R, TABLE>::fns();                                          \
     }

@@ -148,6 +148,23 @@ int spx_ns_stage(const void* state, const void* w0, const void* f0, void* out_f,
                  const void* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
                  int n, int batch, int stage, hipStream_t stream);
 
+/* --- the radio callers -------------------------------------------------------------------
+ * No counterpart in the reference's FFI: its rf.spectrum and rf.fir (python/spectral/rf.py:94-153)
+ * compose fft_c2c with torch ops. These run each as one kernel on rows of n complex samples, for
+ * the implementations with such kernels (spx_rf_max_nfft(impl) > 0: the Stockham variants), nfft
+ * a power of two from 2 to spx_rf_max_nfft(impl).
+ *   spx_rf_spectrum  y (rows, F, nfft), F = ceil(n / nfft) (1 when n <= nfft): the FFT of frame f
+ *                    of each row, x[f nfft .. f nfft + nfft) zero-padded past n, times window
+ *                    (nfft floats; NULL for the rectangular window).
+ *   spx_rf_fir       y (rows, n): x filtered by a causal FIR of `taps` taps (1 <= taps <= nfft)
+ *                    with zero initial state, by overlap-save in blocks of nfft; h is the nfft-point
+ *                    forward FFT of the taps zero-padded to nfft (complex64). */
+int spx_rf_max_nfft(int impl);
+int spx_rf_spectrum(int impl, const void* x, const float* window, void* y, long long n, int nfft,
+                    long long rows, hipStream_t stream);
+int spx_rf_fir(int impl, const void* x, const void* h, void* y, long long n, int taps, int nfft,
+               long long rows, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
