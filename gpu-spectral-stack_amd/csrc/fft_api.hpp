@@ -17,6 +17,8 @@ constexpr int kFourStepMaxN = kStockhamMaxN * kStockhamMaxN;  // 2^24 (reference
 // C2C sizes above kStockhamMaxN that still run as one kernel per transform (the whole transform
 // in one workgroup's LDS); the four-step split takes over beyond.
 constexpr int kSinglePassMaxN = 16384;
+// Above that, up to kTwoPassMaxN, a column pass and a row pass that stores transposed.
+constexpr int kTwoPassMaxN = 1 << 20;
 
 // reference fft.hpp:14-15, 36-39, 59-60
 using C2cFn = void (*)(const cf32* x, cf32* y, int n, int batch, Direction direction,

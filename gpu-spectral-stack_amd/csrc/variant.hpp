@@ -189,6 +189,59 @@ struct TwiddleRowsIo {
     }
 };
 
+// Four-step rows that also transpose (the second of two passes): T consecutive rows k1 of one
+// n1 x N matrix per workgroup, twiddled on the way in like TwiddleRowsIo, and element k2 of row
+// k1 stored at y[slab n + k1 + n1 k2]. Staged through LDS, the store walks k1 fastest, so every
+// k2 is one run of T * 8 bytes: the transposed layout comes out of the row kernel itself.
+struct TwiddleRowsTransposedIo {
+    static constexpr bool kGroupIsBlock = true;
+    TwiddleRowsIo rows;  // input side: x, the twiddle and the scale
+    long long n;         // n1 * N
+
+    template <class P>
+    static constexpr bool direct_in() { return P::L >= 16; }
+    template <class P>
+    static constexpr bool direct_out() { return false; }
+
+    template <class P>
+    __device__ __forceinline__ cf32 in(long long t, int i) const { return rows.in<P>(t, i); }
+    template <class P>
+    __device__ __forceinline__ void out(long long, int, cf32) const {}
+
+    template <class P, class G>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
+    {
+        rows.load<P, G>(lds, first, count, tid);
+    }
+
+    template <class P, class G>
+    __device__ __forceinline__ void store(cf32* lds, long long first, int count,
+                                          int tid) const
+    {
+        static_assert(G::kT == P::T, "the rows of a workgroup are stored together");
+        constexpr int kTotal = P::T * P::N;
+        static_assert(kTotal % G::kThreads == 0, "whole steps");
+        const long long slab = first / rows.n1;  // T divides n1: one slab per workgroup
+        const int k1 = static_cast<int>(first - slab * rows.n1);
+        cf32* const dst = rows.y + slab * n + k1;
+#pragma unroll
+        for (int k = 0; k < kTotal / G::kThreads; ++k) {
+            const int e = tid + k * G::kThreads;
+            const int u = e % P::T;
+            const int k2 = e / P::T;
+            if (G::kFull || u < count) {
+                st_stream(dst + u + static_cast<long long>(rows.n1) * k2,
+                          cscale(lds[u * P::kStride + pad(k2)], rows.scale));
+            }
+        }
+    }
+};
+
+// Rows of the two-pass split: 1024 lanes holding 16 rows (of 512 or 1024 points), so the
+// transposed store writes 128-byte runs.
+template <int N, int R>
+using TransposedRowsPlan = Plan<N, R, cmax(cmax(R, 4), N * 16 / kMaxBlock), kMaxBlock>;
+
 }  // namespace dev
 
 // Stream-ordered scratch memory for one four-step call: allocated on `stream`, freed on it after
@@ -248,7 +301,48 @@ struct Stockham {
         }
     }
 
-    // Any power of two up to kFourStepMaxN: one kernel up to kSinglePassMaxN, four steps beyond.
+    // n = n1 x n2 in two passes, for kSinglePassMaxN < n <= kTwoPassMaxN: n1-point transforms down
+    // the n2 columns of each n1 x n2 matrix (x -> work), then the twiddled n2-point rows, stored
+    // transposed (work -> y): X[k1 + n1 k2] is row k1's element k2.
+    static void two_pass(const cf32* x, cf32* y, int n, int batch, Direction direction,
+                         hipStream_t stream)
+    {
+        const int n2 = n <= (1 << 18) ? 512 : 1024;
+        const int n1 = n / n2;
+        if (static_cast<long long>(batch) * n1 > INT_MAX
+            || static_cast<long long>(batch) * n2 > INT_MAX) {
+            throw InvalidArgument("fourstep: too many transforms");
+        }
+        const bool inverse = direction == Direction::Inverse;
+        const std::size_t total = static_cast<std::size_t>(n) * static_cast<std::size_t>(batch);
+        StreamWorkspace work(total, stream);
+        columns_impl(x, work.get(), n1, n2, batch, direction, stream, 0, 0);
+        const dev::TwiddleRowsTransposedIo rows{
+            dev::TwiddleRowsIo{work.get(), y, inverse ? 1.0f / static_cast<float>(n2) : 1.0f,
+                               inverse ? 1.0f : -1.0f, n1, 2.0f / static_cast<float>(n)},
+            n};
+        const long long transforms = static_cast<long long>(batch) * n1;
+        if (n2 == 512) {
+            launch_rows<512>(rows, inverse, transforms, stream);
+        } else {
+            launch_rows<1024>(rows, inverse, transforms, stream);
+        }
+    }
+
+    template <int N2>
+    static void launch_rows(const dev::TwiddleRowsTransposedIo& rows, bool inverse,
+                            long long transforms, hipStream_t stream)
+    {
+        using P = dev::TransposedRowsPlan<N2, R>;
+        if (inverse) {
+            dev::launch<P, true, Table>(rows, transforms, stream);
+        } else {
+            dev::launch<P, false, Table>(rows, transforms, stream);
+        }
+    }
+
+    // Any power of two up to kFourStepMaxN: one kernel up to kSinglePassMaxN, two passes up to
+    // kTwoPassMaxN, four steps beyond.
     static void c2c(const cf32* x, cf32* y, int n, int batch, Direction direction,
                     hipStream_t stream)
     {
@@ -277,7 +371,13 @@ struct Stockham {
             }
             return;
         }
-        constexpr int n2 = kStockhamMaxN;
+        if (n <= kTwoPassMaxN) {
+            two_pass(x, y, n, batch, direction, stream);
+            return;
+        }
+        // Rows of kSinglePassMaxN points (one kernel each), so the columns are short (n1 <= 1024
+        // for n <= 2^24) and a column workgroup still reads runs of at least 64 bytes.
+        constexpr int n2 = kSinglePassMaxN;
         const int n1 = n / n2;
         if (static_cast<long long>(batch) * n1 > INT_MAX
             || static_cast<long long>(batch) * n2 > INT_MAX) {
@@ -294,8 +394,13 @@ struct Stockham {
                                       inverse ? 1.0f : -1.0f,
                                       n1,
                                       2.0f / static_cast<float>(n)};
-        dev::dispatch_dir<R, Table>(n2, inverse, rows, static_cast<long long>(batch) * n1,
-                                    stream);
+        if (inverse) {
+            dev::dispatch_large<R, true, Table>(n2, rows, static_cast<long long>(batch) * n1,
+                                                stream);
+        } else {
+            dev::dispatch_large<R, false, Table>(n2, rows, static_cast<long long>(batch) * n1,
+                                                 stream);
+        }
         // 4. Row k1, column k2 holds X[k1 + n1 k2]: transpose each matrix (work -> y).
         transpose(work.get(), y, n1, n2, batch, stream);
     }

@@ -21,8 +21,10 @@ pytestmark = pytest.mark.gpu
 IMPLS = spectral.FFT_IMPLS
 SIZES = [1, *POW2_SIZES]
 STOCKHAM = [impl for impl in IMPLS if impl.startswith("stockham")]
-# 8192 and 16384 run as one kernel per transform (a workgroup's LDS holds it); beyond, four-step.
-LARGE_SIZES = [8192, 16384, 32768, 1 << 16, 1 << 20]
+# 8192 and 16384 run as one kernel per transform (a workgroup's LDS holds it); up to 2^20 as a
+# column pass and a transposing row pass (512-point rows up to 2^18, 1024-point beyond); larger
+# sizes as four steps with 16384-point rows.
+LARGE_SIZES = [8192, 16384, 32768, 1 << 16, 1 << 17, 1 << 18, 1 << 19, 1 << 20, 1 << 22]
 
 
 def run(x: np.ndarray, *, inverse: bool = False, impl: str) -> np.ndarray:
@@ -89,7 +91,7 @@ def test_single_pass_large_sizes_over_many_workgroups(rng, impl, n, batch, inver
 
 @pytest.mark.parametrize("impl", IMPLS)
 def test_largest_size(rng, impl):
-    n = 1 << 24  # 4096 x 4096 in the four-step split
+    n = 1 << 24  # 1024 x 16384 in the four-step split
     x = random_complex(rng, (1, n))
     assert_transform_close(run(x, impl=impl), ref.fft(x), n)
 
