@@ -95,6 +95,16 @@ bool fused(const FftImpl& impl, Columns columns, int n1, int n2)
     return columns == Columns::Strided && impl.fused != nullptr && impl.fused->supports(n1, n2);
 }
 
+// Otherwise, from n2 = 32, column-first (fft2_pairs.hpp): columns over the real array read as
+// n1 x n2/2 complex values, whose rows are whole 128-byte lines, and one row-pair pass on the
+// other side; the row-then-column order would run its column pass over half-spectrum rows of
+// n2/2 + 1 values, misaligned.
+bool column_first(const FftImpl& impl, Columns columns, int n1, int n2)
+{
+    return columns == Columns::Strided && impl.fused != nullptr && !impl.fused->supports(n1, n2)
+           && n2 >= 32;
+}
+
 }  // namespace
 
 void transpose(const cf32* x, cf32* y, int rows, int cols, int batch, hipStream_t stream)
@@ -137,6 +147,9 @@ std::size_t fft2_r2c_workspace(const FftImpl& impl, Columns columns, int n1, int
     if (fused(impl, columns, n1, n2)) {
         return 0;
     }
+    if (column_first(impl, columns, n1, n2)) {
+        return count(n1, n2 / 2, batch);
+    }
     const std::size_t half = columns == Columns::Strided ? 0 : 2 * count(n1, n2 / 2 + 1, batch);
     return half + real_work(impl, n1, n2, batch);
 }
@@ -148,6 +161,12 @@ void fft2_r2c(const FftImpl& impl, Columns columns, const float* x, cf32* y, int
     const int w = n2 / 2 + 1;
     if (fused(impl, columns, n1, n2)) {
         impl.fused->r2c(x, y, n1, n2, 0, w, batch, stream);
+        return;
+    }
+    if (column_first(impl, columns, n1, n2)) {
+        impl.columns(reinterpret_cast<const cf32*>(x), work, n1, n2 / 2, batch,
+                     Direction::Forward, stream);
+        impl.fused->r2c_rows(work, y, n1, n2 / 2, batch, stream);
         return;
     }
     if (columns == Columns::Strided) {
@@ -181,6 +200,13 @@ void fft2_c2r(const FftImpl& impl, Columns columns, const cf32* x, float* y, int
     const int w = n2 / 2 + 1;
     if (fused(impl, columns, n1, n2)) {
         impl.fused->c2r(x, y, n1, n2, 0, w, batch, stream);
+        return;
+    }
+    if (column_first(impl, columns, n1, n2)) {
+        // The workspace holds n1 x (n2/2 + 1) per array, more than the n1 x n2/2 used here.
+        impl.fused->c2r_rows(x, work, n1, n2 / 2, batch, stream);
+        impl.columns(work, reinterpret_cast<cf32*>(y), n1, n2 / 2, batch, Direction::Inverse,
+                     stream);
         return;
     }
     const std::size_t q = count(n1, w, batch);

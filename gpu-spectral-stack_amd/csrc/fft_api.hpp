@@ -50,6 +50,11 @@ struct Fused2dFns {
                 hipStream_t stream);
     void (*c2r)(const cf32* x, float* y, int n1, int n2, int m1, int w, int batch,
                 hipStream_t stream);
+    // Row-pair passes of the column-first 2D real transforms (fft2_pairs.hpp), m = n2 / 2 from
+    // 16 to 4096: z (batch x n1 x m, column-transformed packed rows) -> y (batch x n1 x (m + 1)),
+    // and x (batch x n1 x (m + 1)) -> z (prepared, row-inverted, scaled by 1 / m).
+    void (*r2c_rows)(const cf32* z, cf32* y, int n1, int m, int batch, hipStream_t stream);
+    void (*c2r_rows)(const cf32* x, cf32* z, int n1, int m, int batch, hipStream_t stream);
 };
 
 // The radio callers (rf.hpp): windowed spectrum of back-to-back frames, and overlap-save FIR.

@@ -8,6 +8,7 @@
 // real.cu:160-180, fourstep.cuh:110-131): callers and tests match on them.
 
 #include "fft2_fused.hpp"
+#include "fft2_pairs.hpp"
 #include "fft_api.hpp"
 #include "rf.hpp"
 #include "stockham.hpp"
@@ -603,7 +604,49 @@ struct Fused2dDriver {
     }
 
     // Not constexpr, like Stockham::pruned_fns: host function addresses only.
-    static Fused2dFns fns() { return {&supports, &r2c, &c2r}; }
+    // Row-pair passes (fft2_pairs.hpp).
+    template <class Io>
+    static void pairs(int m, bool inverse, const Io& io, long long transforms,
+                      hipStream_t stream)
+    {
+        switch (m) {
+#define SPX_CASE(M)                                                                   \
+    case M:                                                                           \
+        if (inverse) {                                                                \
+            dev::launch<dev::PairPlan<M, R>, true, Table>(io, transforms, stream);    \
+        } else {                                                                      \
+            dev::launch<dev::PairPlan<M, R>, false, Table>(io, transforms, stream);   \
+        }                                                                             \
+        break;
+            SPX_CASE(16)
+            SPX_CASE(32)
+            SPX_CASE(64)
+            SPX_CASE(128)
+            SPX_CASE(256)
+            SPX_CASE(512)
+            SPX_CASE(1024)
+            SPX_CASE(2048)
+            SPX_CASE(4096)
+#undef SPX_CASE
+        default:
+            throw InvalidArgument("fft2 row pairs: unsupported m " + str(m));
+        }
+    }
+
+    static void r2c_rows(const cf32* z, cf32* y, int n1, int m, int batch, hipStream_t stream)
+    {
+        const dev::PairRows rows{n1, n1 / 2 + 1};
+        pairs(m, false, dev::PairR2cIo{z, y, rows}, 2LL * batch * rows.pairs, stream);
+    }
+
+    static void c2r_rows(const cf32* x, cf32* z, int n1, int m, int batch, hipStream_t stream)
+    {
+        const dev::PairRows rows{n1, n1 / 2 + 1};
+        pairs(m, true, dev::PairC2rIo{x, z, rows, 1.0f / static_cast<float>(m)},
+              2LL * batch * rows.pairs, stream);
+    }
+
+    static Fused2dFns fns() { return {&supports, &r2c, &c2r, &r2c_rows, &c2r_rows}; }
 
     static void c2r(const cf32* x, float* y, int n1, int n2, int m1, int w, int batch,
                     hipStream_t stream)

@@ -164,3 +164,26 @@ def test_single_pass_rfft2_and_irfft2(rng, impl, n1, n2):
     spectrum = random_complex(rng, (17, n1, n2 // 2 + 1))
     back = spectral.irfft2(cuda(spectrum), n2, impl=impl)
     assert_transform_close(back, ref.irfft2(spectrum, (n1, n2)), n1 * n2, axes=AXES)
+
+
+# Shapes past the single-pass kernels with n2 >= 32 run column-first: columns over the real array
+# read as complex, then one pass over pairs of rows (k1, -k1). n1 = 1 and 2 make every row its own
+# partner; batches of 3 leave the last workgroup's pairs partly empty. The inverse takes random,
+# non-Hermitian spectra: columns 0 and n2/2 are symmetrized across the pair as numpy does.
+COLUMN_FIRST_SHAPES = [(1, 64), (2, 32), (8, 256), (32, 512), (256, 256), (512, 512), (2048, 64),
+                       (16, 4096), (4, 8192)]
+STOCKHAM_IMPLS = [impl for impl in spectral.FFT_IMPLS if impl.startswith("stockham")]
+
+
+@pytest.mark.parametrize("impl", STOCKHAM_IMPLS)
+@pytest.mark.parametrize(("n1", "n2"), COLUMN_FIRST_SHAPES)
+def test_column_first_rfft2_and_irfft2(rng, impl, n1, n2):
+    x = random_real(rng, (3, n1, n2))
+    y = spectral.rfft2(cuda(x), impl=impl)
+    assert_transform_close(y, ref.rfft2(x), n1 * n2, axes=AXES)
+    spectrum = random_complex(rng, (3, n1, n2 // 2 + 1))
+    back = spectral.irfft2(cuda(spectrum), n2, impl=impl)
+    assert_transform_close(back, ref.irfft2(spectrum, (n1, n2)), n1 * n2, axes=AXES)
+    hermitian = ref.rfft2(x).astype(np.complex64)
+    again = spectral.irfft2(cuda(hermitian), n2, impl=impl)
+    assert_transform_close(again, x, n1 * n2, tol=2 * fft_tolerance(n1 * n2), axes=AXES)
