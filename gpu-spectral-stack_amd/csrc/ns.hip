@@ -7,50 +7,56 @@
 // State: omega_hat on the 2/3-rule modes in the layout of rfft2_truncated with m = n/3 + 1 (rows
 // ky = 0 .. m-1 then -m .. -1, columns kx = 0 .. m-1), (2m) x m complex values per field.
 //
-// Per field (one workgroup):
+// Per field (one workgroup, one lane group per grid row and per kept column):
 //   load W = omega_hat (LDS)
-//   pass A: inverse columns of u_hat = i ky psi_hat and wx_hat = i kx omega_hat (psi_hat =
-//           omega_hat / |k|^2) into tiles T1, T2 (n rows x m columns); then per row, the c2r of
-//           both rows and their product u wx, kept in registers
-//   pass B: the same for v_hat = -i kx psi_hat and wy_hat = i ky omega_hat, adding v wy; then per
-//           row the r2c of the product (still in registers), its first m bins into T1
-//   columns: forward transforms of T1's m columns, then the epilogue on the kept rows:
+//   for each derived field d = u = i ky psi_hat, wx = i kx omega_hat, v = -i kx psi_hat,
+//   wy = i ky omega_hat (psi_hat = omega_hat / |k|^2), one at a time through one tile T
+//   (n rows x m columns):
+//     columns: the inverse column transforms of d's m kept columns into T (one pass)
+//     rows:    per grid row, the c2r of T's row into registers (one pass); the products u wx
+//              and then v wy accumulate in registers
+//   forward: per row, the r2c of the product (still in registers), its first m bins into T;
+//   then the forward transforms of T's m columns, and the epilogue on the kept modes:
 //           F = f_hat - mask N_hat, and the IMEX update
 //             stage 0: out_f = F, out_w = w* = (e w + dt F) i
 //             stage 1: out_w = w' = (e w + dt/2 (f0 + F)) i
 //           with e = 1 + dt/2 L, i = 1 / (1 - dt/2 L), L = -nu |k|^2 - alpha.
+// One field at a time keeps the LDS to W, T and a scratch row per grid row (144 KB at n = 128),
+// so every row phase and every column phase is a single pass of the workgroup: the stage is a
+// chain of dependent LDS passes, and their number is what sets its time.
 // Normalization: inverse 1 / n^2 over the column and row passes, forward none, as numpy.
 
 #include "stockham.hpp"
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 namespace spx {
 namespace dev {
 namespace {
 
-template <int N_>
+template <int N_, int RR = 8, int ER = 8, int RC = 8, int EC = 8>
 struct NsPlan {
     static constexpr int N = N_;
     static constexpr int M = N / 2;         // complex values per real row
     static constexpr int m = N / 3 + 1;      // kept modes per axis
     static constexpr int rows = 2 * m;       // kept rows
     static constexpr int TS = m | 1;         // tile row stride (odd: columns hit distinct banks)
-    using PR = Plan<M, 8, default_e<M, 8>()>;   // row transforms (M-point complex)
-    using PC = Plan<N, 8, default_e<N, 8>()>;   // column transforms
-    static constexpr int NT = N >= 128 ? 512 : 256;
-    static constexpr int RPP = NT / PR::L;    // rows per pass
-    static constexpr int kRowPasses = N / RPP;
-    static constexpr int CPP = NT / PC::L;    // columns per pass
+    using PR = Plan<M, RR, ER>;              // row transforms (M-point complex)
+    using PC = Plan<N, RC, EC>;              // column transforms
+    static constexpr int NT = N * PR::L;     // one lane group per grid row
+    static constexpr int CPP = NT / PC::L;   // columns per pass
     static constexpr int RS = (pad(M) + 1) | 1;  // scratch row stride
-    // LDS layout, in complex values
+    // LDS layout, in complex values: W, the tile, a scratch row per grid row
     static constexpr int kW = rows * m;
     static constexpr int kT = N * TS;
-    static constexpr int kS = RPP * RS;
-    static constexpr int kLds = kW + 2 * kT + kS;
+    static constexpr int kS = N * RS;
+    static constexpr int kLds = kW + kT + kS;
 
     static_assert(PR::L <= 64 && PC::L <= 64, "wave-local transforms");
-    static_assert(N % RPP == 0, "row passes cover the rows");
+    static_assert(NT <= 1024, "one workgroup");
+    static_assert(CPP >= m, "one column pass per field");
     static_assert(kLds * sizeof(cf32) <= 160 * 1024, "LDS budget");
 };
 
@@ -97,33 +103,28 @@ __device__ __forceinline__ cf32 derived(const cf32* W, int r, int c, int which)
     }
 }
 
-// Inverse column transforms of two derived fields (first, first + 1) into T1 and T2.
+// Inverse column transforms of derived field `which` (its m kept columns) into T.
 template <class NP>
-__device__ __forceinline__ void inverse_columns(const cf32* W, cf32* T1, cf32* T2, int first,
-                                                int tid)
+__device__ __forceinline__ void inverse_columns(const cf32* W, cf32* T, int which, int tid)
 {
     using PC = typename NP::PC;
     constexpr int R0 = PC::template radix<0>();
-    for (int g0 = 0; g0 < 2 * NP::m; g0 += NP::CPP) {
-        const int g = g0 + tid / PC::L;
-        const int lane = tid % PC::L;
-        if (g < 2 * NP::m) {
-            const int f = g / NP::m;
-            const int c = g - f * NP::m;
-            cf32 v[PC::E];
+    const int c = tid / PC::L;
+    const int lane = tid % PC::L;
+    if (c < NP::m) {
+        cf32 v[PC::E];
 #pragma unroll
-            for (int b = 0; b < PC::E / R0; ++b) {
+        for (int b = 0; b < PC::E / R0; ++b) {
 #pragma unroll
-                for (int r = 0; r < R0; ++r) {
-                    const int mr = mode_row<NP>(input_index<PC, 0>(lane, b, r));
-                    v[b * R0 + r] = mr >= 0 ? derived<NP>(W, mr, c, first + f) : czero();
-                }
+            for (int r = 0; r < R0; ++r) {
+                const int mr = mode_row<NP>(input_index<PC, 0>(lane, b, r));
+                v[b * R0 + r] = mr >= 0 ? derived<NP>(W, mr, c, which) : czero();
             }
-            cf32* const s = (f == 0 ? T1 : T2) + c;
-            run_stages<PC, 0, true, false, Strided<NP::TS>>(v, s, lane, nullptr);
-            lds_sync<true>();
-            final_write<PC, Strided<NP::TS>>(s, v, lane);
         }
+        cf32* const s = T + c;
+        run_stages<PC, 0, true, false, Strided<NP::TS>>(v, s, lane, nullptr);
+        lds_sync<true>();
+        final_write<PC, Strided<NP::TS>>(s, v, lane);
     }
 }
 
@@ -174,9 +175,8 @@ __global__ void __launch_bounds__(NP::NT)
     static_assert(slots_match<PR>(), "row inverse outputs must be the row forward's inputs");
     __shared__ cf32 lds[NP::kLds];
     cf32* const W = lds;
-    cf32* const T1 = W + NP::kW;
-    cf32* const T2 = T1 + NP::kT;
-    cf32* const S = T2 + NP::kT;
+    cf32* const T = W + NP::kW;
+    cf32* const S = T + NP::kT;
 
     const int tid = threadIdx.x;
     const long long field = blockIdx.x;
@@ -189,42 +189,41 @@ __global__ void __launch_bounds__(NP::NT)
     __syncthreads();
 
     constexpr float kInvScale = 1.0f / static_cast<float>(NP::N * NP::M);
+    const int y = tid / PR::L;  // this lane group's grid row
     const int rlane = tid % PR::L;
-    cf32* const s = S + (tid / PR::L) * NP::RS;
-    cf32 nl[NP::kRowPasses][PR::E];
+    cf32* const s = S + y * NP::RS;
+    cf32* const trow = T + y * NP::TS;
 
-    // Pass A: u and wx, their product per point.
-    inverse_columns<NP>(W, T1, T2, 0, tid);
-    __syncthreads();
+    // u wx + v wy, one derived field at a time: columns into T, then each row's c2r.
+    cf32 nl[PR::E];
+    cf32 first[PR::E];
+#pragma unroll 1
+    for (int which = 0; which < 4; ++which) {
+        inverse_columns<NP>(W, T, which, tid);
+        __syncthreads();
+        cf32 v[PR::E];
+        row_c2r<NP>(trow, s, v, rlane, kInvScale);
+        if (which == 0 || which == 2) {
 #pragma unroll
-    for (int p = 0; p < NP::kRowPasses; ++p) {
-        const int y = p * NP::RPP + tid / PR::L;
-        cf32 a[PR::E];
-        cf32 b[PR::E];
-        row_c2r<NP>(T1 + y * NP::TS, s, a, rlane, kInvScale);
-        row_c2r<NP>(T2 + y * NP::TS, s, b, rlane, kInvScale);
+            for (int e = 0; e < PR::E; ++e) {
+                first[e] = v[e];
+            }
+        } else {
 #pragma unroll
-        for (int e = 0; e < PR::E; ++e) {
-            nl[p][e] = cf32{a[e].re * b[e].re, a[e].im * b[e].im};
+            for (int e = 0; e < PR::E; ++e) {
+                const cf32 p{first[e].re * v[e].re, first[e].im * v[e].im};
+                nl[e] = which == 1 ? p : cf32{nl[e].re + p.re, nl[e].im + p.im};
+            }
         }
+        __syncthreads();  // every row has read T before the next field's columns overwrite it
     }
-    __syncthreads();
 
-    // Pass B: v and wy; add v wy, then the forward row transform of the product.
-    inverse_columns<NP>(W, T1, T2, 2, tid);
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < NP::kRowPasses; ++p) {
-        const int y = p * NP::RPP + tid / PR::L;
-        cf32 a[PR::E];
-        cf32 b[PR::E];
-        row_c2r<NP>(T1 + y * NP::TS, s, a, rlane, kInvScale);
-        row_c2r<NP>(T2 + y * NP::TS, s, b, rlane, kInvScale);
+    // Forward row transform of the product, its first m bins into T.
+    {
         cf32 v[PR::E];
         static_for<0, PR::E>([&](auto ei) {
             constexpr int e = decltype(ei)::value;
-            constexpr int slot = forward_slot_of<PR>(e);
-            v[slot] = cf32{nl[p][e].re + a[e].re * b[e].re, nl[p][e].im + a[e].im * b[e].im};
+            v[forward_slot_of<PR>(e)] = nl[e];
         });
         run_stages<PR, 0, false, false>(v, s, rlane, nullptr);
         lds_sync<true>();
@@ -237,24 +236,22 @@ __global__ void __launch_bounds__(NP::NT)
             const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
             const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
             const cf32 wo = cmul(twiddle_of<2 * M, false>(k), od);
-            cf32* const out = T1 + y * NP::TS;
             if (k < NP::m) {
-                out[k] = cadd(ev, wo);
+                trow[k] = cadd(ev, wo);
             }
             if (k < M - k && M - k < NP::m) {
-                out[M - k] = cconj(csub(ev, wo));
+                trow[M - k] = cconj(csub(ev, wo));
             }
         }
-        lds_sync<true>();
     }
     __syncthreads();
 
-    // Forward columns of the product's row spectra, in place in T1.
-    for (int c0 = 0; c0 < NP::m; c0 += NP::CPP) {
-        const int c = c0 + tid / PC::L;
+    // Forward columns of the product's row spectra, in place in T.
+    {
+        const int c = tid / PC::L;
         const int lane = tid % PC::L;
         if (c < NP::m) {
-            cf32* const col = T1 + c;
+            cf32* const col = T + c;
             cf32 v[PC::E];
             stage_read<PC, 0, Strided<NP::TS>>(col, v, lane);
             run_stages<PC, 0, false, false, Strided<NP::TS>>(v, col, lane, nullptr);
@@ -274,7 +271,7 @@ __global__ void __launch_bounds__(NP::NT)
         const float kx = static_cast<float>(c);
         const int i = r < NP::m ? r : r - 2 * NP::m + NP::N;
         const bool kept = fabsf(kx) <= kmax && fabsf(ky) <= kmax;
-        const cf32 nlh = kept ? T1[i * NP::TS + c] : czero();
+        const cf32 nlh = kept ? T[i * NP::TS + c] : czero();
         const cf32 fh = forcing_hat[e];
         const cf32 F = csub(fh, nlh);
         const float linear = -nu_f * (kx * kx + ky * ky) - drag;
@@ -297,7 +294,11 @@ void launch(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32
             const cf32* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
             int batch, int stage, hipStream_t stream)
 {
-    using NP = NsPlan<N>;
+    // Measured on MI355X (one stage, 256 fields): at n = 128, radix 8 with 8 values per lane
+    // (1024 lanes) took 34.8 us; radix 16 or 16 values per lane (fewer exchanges, 512 lanes, or
+    // spills at 1024) took 37.6-41.8 us. At n = 64, radix 4 with 4 values per lane (512 lanes)
+    // took 14.8 us against 16.8 us for radix 8 (256 lanes).
+    using NP = std::conditional_t<N == 64, NsPlan<64, 4, 4, 4, 4>, NsPlan<N, 8, 8, 8, 8>>;
     hipLaunchKernelGGL(ns_stage_kernel<NP>, dim3(static_cast<unsigned>(batch)), dim3(NP::NT), 0,
                        stream, state, w0, f0, out_f, out_w, forcing_hat, nu, nu_stride, drag, dt,
                        stage);
