@@ -233,6 +233,91 @@ __global__ void __launch_bounds__(kThreads)
         y + row);
 }
 
+// Full-width n = 2 and n = 4 inverses staged through LDS, so every global access is a 16-byte
+// vector at unit stride across the lanes: rows of 2 complex (n = 2) or 3 complex (n = 4) values
+// are read flat as float4s, each lane then takes its rows from LDS. The per-row kernels above
+// store 8 bytes per lane (n = 2) or load three strided 8-byte values per lane (n = 4); measured
+// 70.5 % and 68.8 % of peak at 2^24 points.
+constexpr int kStagedRows2 = 2 * kThreads;  // n = 2: two rows per lane, one float4 out
+constexpr int kStagedRows4 = kThreads;      // n = 4: one row per lane, one float4 out
+
+__global__ void __launch_bounds__(kThreads)
+    c2r_n2_staged_kernel(const f4v* __restrict__ x, f4v* __restrict__ y, std::size_t rows)
+{
+    __shared__ f4v lds[kStagedRows2];
+    const std::size_t first = blockIdx.x * static_cast<std::size_t>(kStagedRows2);
+    const int tid = threadIdx.x;
+    const std::size_t left = rows - first;
+    const int count = left < kStagedRows2 ? static_cast<int>(left) : kStagedRows2;
+    f4v v[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int r = tid + k * kThreads;
+        v[k] = r < count ? __builtin_nontemporal_load(x + first + r) : f4v{};
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        lds[tid + k * kThreads] = v[k];
+    }
+    __syncthreads();
+    const int r = 2 * tid;
+    if (r < count) {
+        const f4v p = lds[r];
+        const f4v q = lds[r + 1];  // beyond count: unused
+        const f4v out{0.5f * (p.x + p.z), 0.5f * (p.x - p.z), 0.5f * (q.x + q.z),
+                      0.5f * (q.x - q.z)};
+        if (r + 1 < count) {
+            __builtin_nontemporal_store(out, y + (first + r) / 2);
+        } else {
+            __builtin_nontemporal_store(f2v{out.x, out.y},
+                                        reinterpret_cast<f2v*>(y) + first + r);
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+    c2r_n4_staged_kernel(const float* __restrict__ x, f4v* __restrict__ y, std::size_t rows)
+{
+    constexpr int kFloats = 6 * kStagedRows4;  // 3 complex values per row
+    __shared__ float lds[kFloats];
+    const std::size_t first = blockIdx.x * static_cast<std::size_t>(kStagedRows4);
+    const int tid = threadIdx.x;
+    const std::size_t left = rows - first;
+    const int count = left < kStagedRows4 ? static_cast<int>(left) : kStagedRows4;
+    const float* src = x + first * 6;
+    if (count == kStagedRows4) {
+        const f4v* src4 = reinterpret_cast<const f4v*>(src);  // 6 kThreads floats, 16-byte aligned
+        f4v v[kFloats / 4 / kThreads + 1];
+#pragma unroll
+        for (int k = 0; k * kThreads < kFloats / 4; ++k) {
+            const int i = tid + k * kThreads;
+            v[k] = i < kFloats / 4 ? __builtin_nontemporal_load(src4 + i) : f4v{};
+        }
+#pragma unroll
+        for (int k = 0; k * kThreads < kFloats / 4; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < kFloats / 4) {
+                reinterpret_cast<f4v*>(lds)[i] = v[k];
+            }
+        }
+    } else {
+        for (int i = tid; i < 6 * count; i += kThreads) {
+            lds[i] = src[i];
+        }
+    }
+    __syncthreads();
+    if (tid < count) {
+        const float* in = lds + 6 * tid;
+        const float ac = in[0] + in[4];
+        const float amc = in[0] - in[4];
+        const float p2 = 2.0f * in[2];
+        const float q2 = 2.0f * in[3];
+        __builtin_nontemporal_store(
+            f4v{0.25f * (ac + p2), 0.25f * (amc - q2), 0.25f * (ac - p2), 0.25f * (amc + q2)},
+            y + first + tid);
+    }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -256,6 +341,13 @@ void c2r_n2(const cf32* x, float* y, int batch, int keep, hipStream_t stream)
     const auto rows = static_cast<std::size_t>(batch);
     const dim3 grid(static_cast<unsigned>((rows + kThreads - 1) / kThreads));
     auto* yv = reinterpret_cast<f2v*>(y);
+    if (keep == 2 && aligned16(x) && aligned16(y)) {
+        const dim3 staged(static_cast<unsigned>((rows + kStagedRows2 - 1) / kStagedRows2));
+        hipLaunchKernelGGL(c2r_n2_staged_kernel, staged, dim3(kThreads), 0, stream,
+                           reinterpret_cast<const f4v*>(x), reinterpret_cast<f4v*>(y), rows);
+        SPX_LAUNCH_CHECK();
+        return;
+    }
     if (aligned16(x)) {
         hipLaunchKernelGGL(c2r_n2_kernel<true>, grid, dim3(kThreads), 0, stream, x, yv, keep, rows);
     } else {
@@ -271,6 +363,13 @@ bool c2r_n4(const cf32* x, float* y, int batch, int keep, hipStream_t stream)
         return false;  // the caller runs the general kernel instead
     }
     const auto rows = static_cast<std::size_t>(batch);
+    if (keep == 3 && aligned16(x)) {
+        const dim3 staged(static_cast<unsigned>((rows + kStagedRows4 - 1) / kStagedRows4));
+        hipLaunchKernelGGL(c2r_n4_staged_kernel, staged, dim3(kThreads), 0, stream,
+                           reinterpret_cast<const float*>(x), reinterpret_cast<f4v*>(y), rows);
+        SPX_LAUNCH_CHECK();
+        return true;
+    }
     const dim3 grid(static_cast<unsigned>((rows + kThreads - 1) / kThreads));
     hipLaunchKernelGGL(c2r_n4_kernel, grid, dim3(kThreads), 0, stream, x,
                        reinterpret_cast<f4v*>(y), keep, rows);
