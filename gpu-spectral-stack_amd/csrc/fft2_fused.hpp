@@ -53,7 +53,11 @@ struct Fused2d {
     using PC = Plan<N1, R, (N1 >= 128 ? cmax(16, default_e<N1, R>()) : default_e<N1, R>())>;
     static constexpr int TS = (pad(M) + 1) | 1;    // tile row stride, odd
     static constexpr int kTile = N1 * TS;          // complex values per array
-    static constexpr int AP = cmax(1, 16384 / (N1 * N2));  // arrays per workgroup
+    // Arrays per workgroup: about 16384 points, as many as the 80 KB tile budget allows (a
+    // power of two, so the row passes still cover the rows exactly).
+    static constexpr int kLdsArrays = 80 * 1024 / (kTile * static_cast<int>(sizeof(cf32)));
+    static constexpr int AP = cmin(cmax(1, 16384 / (N1 * N2)),
+                                   1 << (31 - __builtin_clz(cmax(1, kLdsArrays))));
     static constexpr int NT = 512;                 // lanes per workgroup
     static constexpr int NW = NT / 64;
     static constexpr int kRows = AP * N1;
@@ -112,11 +116,11 @@ __device__ __forceinline__ void prepare_row(cf32* s, int k, int w)
 }
 
 // Forward: z = the real arrays viewed as complex (batch x N1 x M), y = batch arrays of rows_out x w
-// values (rows_out = 2 m1 when m1 > 0, else N1).
+// values (rows_out = 2 m1 when m1 > 0, else N1). wdiv divides by w, odiv by rows_out w.
 template <class F>
 __global__ void __launch_bounds__(F::NT)
     rfft2_fused_kernel(const cf32* __restrict__ z, cf32* __restrict__ y, int m1, int w,
-                       FastDiv wdiv, long long batch, const cf32* table)
+                       FastDiv wdiv, FastDiv odiv, long long batch, const cf32* table)
 {
     using PR = typename F::PR;
     using PC = typename F::PC;
@@ -178,16 +182,32 @@ __global__ void __launch_bounds__(F::NT)
     }
     __syncthreads();
 
-    // Store the kept rows of the first w columns: one wave per output row, lanes along the row.
-    const int rows_out = m1 > 0 ? 2 * m1 : F::N1;
-    const int wave = tid / 64;
-    const int lane = tid % 64;
-    for (int a = 0; a < count; ++a) {
-        cf32* const dst = y + (first + a) * rows_out * w;
-        for (int f = wave; f < rows_out; f += F::NW) {
-            const cf32* src = tile + a * F::kTile + F::row_of(f, m1) * F::TS;
-            for (int c = lane; c < w; c += 64) {
-                st_stream(dst + f * w + c, src[pad(c)]);
+    // Store the kept rows of the first w columns. The workgroup's output is one contiguous run of
+    // count x rows_out x w values: the lanes walk it flat, coalesced whatever w is (rows of a
+    // few values, as at 4 x 4, would otherwise leave most of a wave idle), reading kStoreChunk
+    // tile values into registers before storing them.
+    const int per_array = (m1 > 0 ? 2 * m1 : F::N1) * w;
+    const int total = count * per_array;
+    cf32* const dst = y + first * per_array;
+    constexpr int kStoreChunk = 8;
+#pragma unroll 1
+    for (int e0 = 0; e0 < total; e0 += F::NT * kStoreChunk) {
+        cf32 val[kStoreChunk];
+#pragma unroll
+        for (int k = 0; k < kStoreChunk; ++k) {
+            const int e = e0 + k * F::NT + tid;
+            if (e < total) {
+                const int a = static_cast<int>(odiv.div(static_cast<unsigned>(e)));
+                const int r = e - a * per_array;
+                const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(r)));
+                val[k] = tile[a * F::kTile + F::row_of(f, m1) * F::TS + pad(r - f * w)];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kStoreChunk; ++k) {
+            const int e = e0 + k * F::NT + tid;
+            if (e < total) {
+                st_stream(dst + e, val[k]);
             }
         }
     }
@@ -208,8 +228,6 @@ __global__ void __launch_bounds__(F::NT)
     const long long first = static_cast<long long>(blockIdx.x) * F::AP;
     const int count = static_cast<int>(batch - first < F::AP ? batch - first : F::AP);
     const int tid = threadIdx.x;
-    const int wave = tid / 64;
-    const int lane64 = tid % 64;
 
     // Load the kept rows of the first w columns (contiguous in x: count arrays of rows_in x w),
     // every lane's loads in flight before any LDS write; then zero the dropped rows.
@@ -234,20 +252,12 @@ __global__ void __launch_bounds__(F::NT)
             tile[a * F::kTile + F::row_of(f, m1) * F::TS + pad(c)] = val[k];
         }
     }
-    if (m1 > 0) {
-        for (int a = 0; a < count; ++a) {
-            for (int i = m1 + wave; i < F::N1 - m1; i += F::NW) {
-                cf32* const d = tile + a * F::kTile + i * F::TS;
-                for (int c = lane64; c < w; c += 64) {
-                    d[pad(c)] = czero();
-                }
-            }
-        }
-    }
     __syncthreads();
 
-    // Inverse columns 0 .. w-1, in place.
+    // Inverse columns 0 .. w-1, in place. The dropped rows (m1 > 0) are read as zeros, never
+    // from the tile: the column's later stages overwrite all its rows anyway.
     const int total_cols = F::AP * w;
+    constexpr int R0 = PC::template radix<0>();
 #pragma unroll 1
     for (int c0 = 0; c0 < total_cols; c0 += F::CPP) {
         const int cg = c0 + tid / PC::L;
@@ -257,7 +267,15 @@ __global__ void __launch_bounds__(F::NT)
             const int c = cg - a * w;
             cf32* const s = tile + a * F::kTile + pad(c);
             cf32 v[PC::E];
-            stage_read<PC, 0, Strided<F::TS>>(s, v, lane);
+#pragma unroll
+            for (int b = 0; b < PC::E / R0; ++b) {
+#pragma unroll
+                for (int r = 0; r < R0; ++r) {
+                    const int i = input_index<PC, 0>(lane, b, r);
+                    const bool kept = m1 == 0 || i < m1 || i >= F::N1 - m1;
+                    v[b * R0 + r] = kept ? s[i * F::TS] : czero();
+                }
+            }
             run_stages<PC, 0, true, F::kTable, Strided<F::TS>>(v, s, lane, table);
             lds_sync<true>();
             final_write<PC, Strided<F::TS>>(s, v, lane);

@@ -515,9 +515,10 @@ struct Stockham {
     }
 };
 
-// The (n1, n2) shapes with a single-pass 2D kernel: both in 32 .. 256 and the half spectrum (plus
-// row padding) within the 80 KB LDS tile of fft2_fused.hpp.
+// The (n1, n2) shapes with a single-pass 2D kernel: both in 4 .. 16, or both in 32 .. 256 with the
+// half spectrum (plus row padding) within the 80 KB LDS tile of fft2_fused.hpp.
 #define SPX_FUSED_SHAPES(X)                                                                     \
+    X(4, 4) X(8, 4) X(16, 4) X(4, 8) X(8, 8) X(16, 8) X(4, 16) X(8, 16) X(16, 16)                \
     X(32, 32) X(64, 32) X(128, 32) X(256, 32) X(32, 64) X(64, 64) X(128, 64) X(256, 64)         \
     X(32, 128) X(64, 128) X(128, 128) X(32, 256) X(64, 256)
 
@@ -566,9 +567,11 @@ struct Fused2dDriver {
         using F = dev::Fused2d<N1, M, R, Table>;
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
         const cf32* table = Table ? twiddle_table() : nullptr;
+        const int rows_out = m1 > 0 ? 2 * m1 : N1;
         hipLaunchKernelGGL((dev::rfft2_fused_kernel<F>), dim3(static_cast<unsigned>(blocks)),
                            dim3(F::NT), 0, stream, reinterpret_cast<const cf32*>(x), y, m1, w,
                            dev::FastDiv::of(static_cast<unsigned>(w)),
+                           dev::FastDiv::of(static_cast<unsigned>(rows_out * w)),
                            static_cast<long long>(batch), table);
         SPX_LAUNCH_CHECK();
     }

@@ -146,9 +146,10 @@ def test_rejects_a_spectrum_of_the_wrong_width():
         spectral.irfft2(x, 8)
 
 
-# Every shape with a single-pass kernel (n1, n2 in 32 .. 256 whose half spectrum fits the LDS
-# tile), with a batch that leaves the last workgroup partly empty (17 = 16 arrays + 1 for 32 x 32).
-FUSED_SHAPES = [(32, 32), (64, 32), (128, 32), (256, 32), (32, 64), (64, 64), (128, 64),
+# Every shape with a single-pass kernel (n1, n2 in 4 .. 16, or in 32 .. 256 with the half spectrum
+# within the LDS tile), with a batch of 17 that leaves the last workgroup partly empty.
+FUSED_SHAPES = [(4, 4), (8, 4), (16, 4), (4, 8), (8, 8), (16, 8), (4, 16), (8, 16), (16, 16),
+                (32, 32), (64, 32), (128, 32), (256, 32), (32, 64), (64, 64), (128, 64),
                 (256, 64), (32, 128), (64, 128), (128, 128), (32, 256), (64, 256)]
 FUSED_IMPLS = ["stockham_r4", "stockham_r8", "stockham_r8_table"]
 

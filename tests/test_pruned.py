@@ -164,7 +164,8 @@ def test_rejects_keep_out_of_range():
 
 
 # Every shape with a single-pass kernel, with random kept-mode counts and a partial last workgroup.
-FUSED_SHAPES = [(32, 32), (64, 32), (128, 32), (256, 32), (32, 64), (64, 64), (128, 64),
+FUSED_SHAPES = [(4, 4), (8, 4), (16, 4), (4, 8), (8, 8), (16, 8), (4, 16), (8, 16), (16, 16),
+                (32, 32), (64, 32), (128, 32), (256, 32), (32, 64), (64, 64), (128, 64),
                 (256, 64), (32, 128), (64, 128), (128, 128), (32, 256), (64, 256)]
 
 
