@@ -129,6 +129,10 @@ void fft2_c2c(const FftImpl& impl, Columns columns, const cf32* x, cf32* y, int 
               int batch, Direction direction, cf32* work, hipStream_t stream)
 {
     check(impl, columns, n1, n2, batch, false);
+    if (columns == Columns::Strided && impl.fused != nullptr && impl.fused->c2c_supports(n1, n2)) {
+        impl.fused->c2c(x, y, n1, n2, batch, direction, stream);
+        return;
+    }
     if (columns == Columns::Strided) {
         impl.c2c(x, y, n2, batch * n1, direction, stream);
         impl.columns(y, y, n1, n2, batch, direction, stream);

@@ -55,6 +55,10 @@ struct Fused2dFns {
     // and x (batch x n1 x (m + 1)) -> z (prepared, row-inverted, scaled by 1 / m).
     void (*r2c_rows)(const cf32* z, cf32* y, int n1, int m, int batch, hipStream_t stream);
     void (*c2r_rows)(const cf32* x, cf32* z, int n1, int m, int batch, hipStream_t stream);
+    // Single-pass complex 2D (batch arrays of n1 x n2) where c2c_supports(n1, n2).
+    bool (*c2c_supports)(int n1, int n2);
+    void (*c2c)(const cf32* x, cf32* y, int n1, int n2, int batch, Direction direction,
+                hipStream_t stream);
 };
 
 // The radio callers (rf.hpp): windowed spectrum of back-to-back frames, and overlap-save FIR.

@@ -522,6 +522,11 @@ struct Stockham {
     X(32, 32) X(64, 32) X(128, 32) X(256, 32) X(32, 64) X(64, 64) X(128, 64) X(256, 64)         \
     X(32, 128) X(64, 128) X(128, 128) X(32, 256) X(64, 256)
 
+// The (n1, n2) shapes with a single-pass complex 2D kernel: an array of n1 x n2 complex values
+// (plus row padding) within the same 80 KB tile.
+#define SPX_FUSED_C2C_SHAPES(X)                                                                 \
+    X(4, 4) X(8, 8) X(16, 16) X(32, 32) X(32, 64) X(64, 32) X(64, 64) X(64, 128) X(128, 64)
+
 // Single-pass 2D drivers of one variant (radix 4 and up; radix 2 has none).
 template <int R, bool Table>
 struct Fused2dDriver {
@@ -607,6 +612,65 @@ struct Fused2dDriver {
     }
 
     // Not constexpr, like Stockham::pruned_fns: host function addresses only.
+    static bool c2c_supports(int n1, int n2)
+    {
+        if constexpr (R >= 4) {
+#define SPX_X(A, B)                 \
+    if (n1 == (A) && n2 == (B)) {   \
+        return true;                \
+    }
+            SPX_FUSED_C2C_SHAPES(SPX_X)
+#undef SPX_X
+        }
+        (void)n1;
+        (void)n2;
+        return false;
+    }
+
+    template <int N1, int N2>
+    static void launch_c2c(const cf32* x, cf32* y, int batch, bool inverse, hipStream_t stream)
+    {
+        using F = dev::Fused2d<N1, N2, R, Table>;  // M = N2: complex rows of n2 values
+        const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
+        const cf32* table = Table ? twiddle_table() : nullptr;
+        const float scale = inverse ? 1.0f / static_cast<float>(N1 * N2) : 1.0f;
+        if (inverse) {
+            hipLaunchKernelGGL((dev::fft2_fused_kernel<F, true>),
+                               dim3(static_cast<unsigned>(blocks)), dim3(F::NT), 0, stream, x, y,
+                               static_cast<long long>(batch), scale, table);
+        } else {
+            hipLaunchKernelGGL((dev::fft2_fused_kernel<F, false>),
+                               dim3(static_cast<unsigned>(blocks)), dim3(F::NT), 0, stream, x, y,
+                               static_cast<long long>(batch), scale, table);
+        }
+        SPX_LAUNCH_CHECK();
+    }
+
+    static void c2c(const cf32* x, cf32* y, int n1, int n2, int batch, Direction direction,
+                    hipStream_t stream)
+    {
+        if (!c2c_supports(n1, n2) || batch < 1) {
+            throw InvalidArgument("fused 2D: no complex kernel for " + str(n1) + " x " + str(n2));
+        }
+        const std::size_t bytes = static_cast<std::size_t>(batch) * n1 * n2 * sizeof(cf32);
+        const auto* a = reinterpret_cast<const char*>(x);
+        const auto* b = reinterpret_cast<const char*>(y);
+        if (a < b + bytes && b < a + bytes) {
+            throw InvalidArgument("fused 2D: input and output must not overlap");
+        }
+        const bool inverse = direction == Direction::Inverse;
+        if constexpr (R >= 4) {
+#define SPX_X(A, B)                                             \
+    if (n1 == (A) && n2 == (B)) {                               \
+        launch_c2c<(A), (B)>(x, y, batch, inverse, stream);     \
+        return;                                                 \
+    }
+            SPX_FUSED_C2C_SHAPES(SPX_X)
+#undef SPX_X
+        }
+        (void)inverse;
+    }
+
     // Row-pair passes (fft2_pairs.hpp).
     template <class Io>
     static void pairs(int m, bool inverse, const Io& io, long long transforms,
@@ -649,7 +713,10 @@ struct Fused2dDriver {
               2LL * batch * rows.pairs, stream);
     }
 
-    static Fused2dFns fns() { return {&supports, &r2c, &c2r, &r2c_rows, &c2r_rows}; }
+    static Fused2dFns fns()
+    {
+        return {&supports, &r2c, &c2r, &r2c_rows, &c2r_rows, &c2c_supports, &c2c};
+    }
 
     static void c2r(const cf32* x, float* y, int n1, int n2, int m1, int w, int batch,
                     hipStream_t stream)

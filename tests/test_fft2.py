@@ -188,3 +188,21 @@ def test_column_first_rfft2_and_irfft2(rng, impl, n1, n2):
     hermitian = ref.rfft2(x).astype(np.complex64)
     again = spectral.irfft2(cuda(hermitian), n2, impl=impl)
     assert_transform_close(again, x, n1 * n2, tol=2 * fft_tolerance(n1 * n2), axes=AXES)
+
+
+# Complex 2D arrays whose n1 x n2 tile fits a workgroup's LDS run as one kernel (fft2_c2c,
+# strided method); batches of 17 leave the last workgroup partly empty.
+FUSED_C2C_SHAPES = [(4, 4), (8, 8), (16, 16), (32, 32), (32, 64), (64, 32), (64, 64), (64, 128),
+                    (128, 64)]
+
+
+@pytest.mark.parametrize("impl", FUSED_IMPLS)
+@pytest.mark.parametrize(("n1", "n2"), FUSED_C2C_SHAPES)
+def test_single_pass_fft2_and_ifft2(rng, impl, n1, n2):
+    x = random_complex(rng, (17, n1, n2))
+    y = spectral.fft2(cuda(x), impl=impl)
+    assert_transform_close(y, ref.fft2(x), n1 * n2, axes=AXES)
+    two_pass = spectral.fft2(cuda(x), impl=impl, columns="transpose")
+    assert_transform_close(y, two_pass.cpu().numpy(), n1 * n2, axes=AXES)
+    back = spectral.fft2(cuda(x), inverse=True, impl=impl)
+    assert_transform_close(back, ref.ifft2(x), n1 * n2, axes=AXES)
