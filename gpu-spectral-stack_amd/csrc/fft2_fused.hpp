@@ -40,7 +40,7 @@ struct FastDiv {
     }
 };
 
-template <int N1_, int M_, int R, bool Table>
+template <int N1_, int M_, int R, bool Table, int BudgetKB = 80>
 struct Fused2d {
     static constexpr int N1 = N1_;                 // rows (column transform length)
     static constexpr int M = M_;                   // complex values per real row (n2 / 2)
@@ -55,7 +55,8 @@ struct Fused2d {
     static constexpr int kTile = N1 * TS;          // complex values per array
     // Arrays per workgroup: about 16384 points, as many as the 80 KB tile budget allows (a
     // power of two, so the row passes still cover the rows exactly).
-    static constexpr int kLdsArrays = 80 * 1024 / (kTile * static_cast<int>(sizeof(cf32)));
+    static constexpr int kLdsArrays =
+        BudgetKB * 1024 / (kTile * static_cast<int>(sizeof(cf32)));
     static constexpr int AP = cmin(cmax(1, 16384 / (N1 * N2)),
                                    1 << (31 - __builtin_clz(cmax(1, kLdsArrays))));
     static constexpr int NT = 512;                 // lanes per workgroup
@@ -67,7 +68,7 @@ struct Fused2d {
 
     static_assert(PR::L <= 64 && PC::L <= 64, "row and column transforms stay inside a wave");
     static_assert(kRows % RPP == 0, "row passes cover the rows exactly");
-    static_assert(AP * kTile * sizeof(cf32) <= 80 * 1024, "tile exceeds the LDS budget");
+    static_assert(AP * kTile * sizeof(cf32) <= BudgetKB * 1024, "tile exceeds the LDS budget");
 
     // Tile row holding frequency-row f of the kept rows (all rows when m1 = 0).
     __device__ __forceinline__ static int row_of(int f, int m1)

@@ -523,9 +523,11 @@ struct Stockham {
     X(32, 128) X(64, 128) X(128, 128) X(32, 256) X(64, 256)
 
 // The (n1, n2) shapes with a single-pass complex 2D kernel: an array of n1 x n2 complex values
-// (plus row padding) within the same 80 KB tile.
+// (plus row padding) within the same 80 KB tile, and 128 x 128 alone in a 140 KB one (one
+// workgroup per CU).
 #define SPX_FUSED_C2C_SHAPES(X)                                                                 \
-    X(4, 4) X(8, 8) X(16, 16) X(32, 32) X(32, 64) X(64, 32) X(64, 64) X(64, 128) X(128, 64)
+    X(4, 4) X(8, 8) X(16, 16) X(32, 32) X(32, 64) X(64, 32) X(64, 64) X(64, 128) X(128, 64)      \
+    X(128, 128)
 
 // Single-pass 2D drivers of one variant (radix 4 and up; radix 2 has none).
 template <int R, bool Table>
@@ -630,7 +632,8 @@ struct Fused2dDriver {
     template <int N1, int N2>
     static void launch_c2c(const cf32* x, cf32* y, int batch, bool inverse, hipStream_t stream)
     {
-        using F = dev::Fused2d<N1, N2, R, Table>;  // M = N2: complex rows of n2 values
+        // M = N2: complex rows of n2 values; 128 x 128 takes a 140 KB tile.
+        using F = dev::Fused2d<N1, N2, R, Table, (N1 * N2 > 8192 ? 160 : 80)>;
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
         const cf32* table = Table ? twiddle_table() : nullptr;
         const float scale = inverse ? 1.0f / static_cast<float>(N1 * N2) : 1.0f;

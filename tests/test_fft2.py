@@ -193,7 +193,7 @@ def test_column_first_rfft2_and_irfft2(rng, impl, n1, n2):
 # Complex 2D arrays whose n1 x n2 tile fits a workgroup's LDS run as one kernel (fft2_c2c,
 # strided method); batches of 17 leave the last workgroup partly empty.
 FUSED_C2C_SHAPES = [(4, 4), (8, 8), (16, 16), (32, 32), (32, 64), (64, 32), (64, 64), (64, 128),
-                    (128, 64)]
+                    (128, 64), (128, 128)]
 
 
 @pytest.mark.parametrize("impl", FUSED_IMPLS)
