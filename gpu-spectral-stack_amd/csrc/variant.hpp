@@ -238,6 +238,101 @@ struct TwiddleRowsTransposedIo {
     }
 };
 
+// One of two passes of a long column transform (n = n1c x n2c points down the columns of
+// slabs x n x cols arrays), each staging whole column runs like StridedIo. Transform t is column
+// c = t mod cols of group g = (t / cols) mod groups of slab t / (cols groups); its element i is
+// read at x[slab slab_elems + g step_in + i stride_in + c] and its output k written at
+// y[slab slab_elems + g step_out + k stride_out + c], times exp(sign 2 pi i g k two_over_n / 2)
+// when twiddled (two_over_n = 2 / n; g k < n, exact in float). With j = j1 n2c + j2 and
+// k = k1 + n1c k2:
+//   pass A: group g = j2, input rows j1 n2c + j2, output rows k1 n2c + j2, twiddle w_n^(j2 k1);
+//   pass B: group g = k1, input rows k1 n2c + j2, output rows k1 + n1c k2 = X[k].
+struct ColumnStepIo {
+    static constexpr bool kGroupIsBlock = true;
+    const cf32* x;
+    cf32* y;
+    int cols;
+    int groups;
+    long long slab_elems;
+    long long step_in;
+    long long stride_in;
+    long long step_out;
+    long long stride_out;
+    float scale;
+    bool twiddle;
+    float sign;
+    float two_over_n;
+
+    template <class P>
+    static constexpr bool direct_in() { return false; }
+    template <class P>
+    static constexpr bool direct_out() { return false; }
+
+    template <class P>
+    __device__ __forceinline__ cf32 in(long long, int) const { return czero(); }
+    template <class P>
+    __device__ __forceinline__ void out(long long, int, cf32) const {}
+
+    // Base offset (without the element term) and group of transform t.
+    __device__ __forceinline__ long long origin(long long t, bool input, int& g) const
+    {
+        const long long q = t / cols;
+        const int c = static_cast<int>(t - q * cols);
+        const long long slab = q / groups;
+        g = static_cast<int>(q - slab * groups);
+        return slab * slab_elems + g * (input ? step_in : step_out) + c;
+    }
+
+    template <class P, class G>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
+    {
+        static_assert(G::kT == P::T, "column runs stage a whole workgroup");
+        constexpr int kRowsPerStep = G::kThreads / P::T;
+        constexpr int kSteps = P::N / kRowsPerStep;
+        const int j = tid % P::T;
+        if (!G::kFull && j >= count) {
+            return;
+        }
+        int g = 0;
+        const cf32* const base = x + origin(first + j, true, g);
+        cf32 val[kSteps];
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            const int i = tid / P::T + k * kRowsPerStep;
+            val[k] = ld_stream(base + i * stride_in);
+        }
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            lds[j * P::kStride + pad(tid / P::T + k * kRowsPerStep)] = val[k];
+        }
+    }
+
+    template <class P, class G>
+    __device__ __forceinline__ void store(cf32* lds, long long first, int count,
+                                          int tid) const
+    {
+        constexpr int kRowsPerStep = G::kThreads / P::T;
+        constexpr int kSteps = P::N / kRowsPerStep;
+        const int j = tid % P::T;
+        if (!G::kFull && j >= count) {
+            return;
+        }
+        int g = 0;
+        cf32* const base = y + origin(first + j, false, g);
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            const int i = tid / P::T + k * kRowsPerStep;
+            cf32 v = cscale(lds[j * P::kStride + pad(i)], scale);
+            if (twiddle) {
+                cf32 w = expi_pi(static_cast<float>(g * i) * two_over_n);
+                w.im *= sign;
+                v = cmul(v, w);
+            }
+            st_stream(base + i * stride_out, v);
+        }
+    }
+};
+
 // Rows of the two-pass split: 1024 lanes holding 16 rows (of 512 or 1024 points), so the
 // transposed store writes 128-byte runs.
 template <int N, int R>
@@ -406,6 +501,57 @@ struct Stockham {
         transpose(work.get(), y, n1, n2, batch, stream);
     }
 
+    // Columns of n = 2048 or 4096 points as two passes of 64 x (n / 64) (four-step on the column
+    // axis): a single pass would stage only 4 or 2 columns per workgroup, reading runs of 32 or
+    // 16 bytes; each of these passes stages 32 columns of 64 points (256-byte runs). Pass A runs
+    // the 64-point transforms over rows j1 (n/64) + j2 and twiddles them (x -> work); pass B runs
+    // the (n/64)-point transforms over rows k1 (n/64) + j2 and writes row k1 + 64 k2 (work -> y).
+    static void long_columns(const cf32* x, cf32* y, int n, int cols, int slabs,
+                             Direction direction, hipStream_t stream)
+    {
+        constexpr int n1c = 64;
+        const int n2c = n / n1c;
+        const bool inverse = direction == Direction::Inverse;
+        const long long slab_elems = static_cast<long long>(n) * cols;
+        const std::size_t total = static_cast<std::size_t>(slab_elems) * slabs;
+        StreamWorkspace work(total, stream);
+        const dev::ColumnStepIo a{x,
+                                  work.get(),
+                                  cols,
+                                  n2c,
+                                  slab_elems,
+                                  cols,
+                                  static_cast<long long>(n2c) * cols,
+                                  cols,
+                                  static_cast<long long>(n2c) * cols,
+                                  1.0f,
+                                  true,
+                                  inverse ? 1.0f : -1.0f,
+                                  2.0f / static_cast<float>(n)};
+        const dev::ColumnStepIo b{work.get(),
+                                  y,
+                                  cols,
+                                  n1c,
+                                  slab_elems,
+                                  static_cast<long long>(n2c) * cols,
+                                  cols,
+                                  cols,
+                                  static_cast<long long>(n1c) * cols,
+                                  inverse ? 1.0f / static_cast<float>(n) : 1.0f,
+                                  false,
+                                  1.0f,
+                                  0.0f};
+        const long long transforms_a = static_cast<long long>(slabs) * n2c * cols;
+        const long long transforms_b = static_cast<long long>(slabs) * n1c * cols;
+        if (inverse) {
+            dev::dispatch_columns<R, true, Table>(n1c, a, transforms_a, stream);
+            dev::dispatch_columns<R, true, Table>(n2c, b, transforms_b, stream);
+        } else {
+            dev::dispatch_columns<R, false, Table>(n1c, a, transforms_a, stream);
+            dev::dispatch_columns<R, false, Table>(n2c, b, transforms_b, stream);
+        }
+    }
+
     static void columns_impl(const cf32* x, cf32* y, int n, int cols, int slabs,
                              Direction direction, hipStream_t stream, int m1_in, int m1_out)
     {
@@ -420,6 +566,10 @@ struct Stockham {
             throw InvalidArgument("stockham columns: a pruned transform cannot run in place");
         }
         const long long batch = static_cast<long long>(cols) * slabs;
+        if (n >= 2048 && m1_in == 0 && m1_out == 0 && cols >= 32) {
+            long_columns(x, y, n, cols, slabs, direction, stream);
+            return;
+        }
         if (n == 1) {
             if (x != y) {
                 SPX_HIP_CHECK(hipMemcpyAsync(y, x, static_cast<std::size_t>(batch) * sizeof(cf32),

@@ -206,3 +206,23 @@ def test_single_pass_fft2_and_ifft2(rng, impl, n1, n2):
     assert_transform_close(y, two_pass.cpu().numpy(), n1 * n2, axes=AXES)
     back = spectral.fft2(cuda(x), inverse=True, impl=impl)
     assert_transform_close(back, ref.ifft2(x), n1 * n2, axes=AXES)
+
+
+# Columns of 2048 and 4096 points run as two passes of 64 x (n1 / 64) (tiles of 32 or more
+# columns), for complex 2D and for the column passes of the real column-first transforms.
+LONG_COLUMN_SHAPES = [(2048, 32), (2048, 64), (4096, 32), (4096, 128)]
+
+
+@pytest.mark.parametrize("impl", STOCKHAM_IMPLS)
+@pytest.mark.parametrize(("n1", "n2"), LONG_COLUMN_SHAPES)
+def test_long_columns(rng, impl, n1, n2):
+    x = random_complex(rng, (2, n1, n2))
+    assert_transform_close(spectral.fft2(cuda(x), impl=impl), ref.fft2(x), n1 * n2, axes=AXES)
+    assert_transform_close(spectral.fft2(cuda(x), inverse=True, impl=impl), ref.ifft2(x),
+                           n1 * n2, axes=AXES)
+    r = random_real(rng, (2, n1, 2 * n2))
+    assert_transform_close(spectral.rfft2(cuda(r), impl=impl), ref.rfft2(r), 2 * n1 * n2,
+                           axes=AXES)
+    spectrum = random_complex(rng, (2, n1, n2 + 1))
+    assert_transform_close(spectral.irfft2(cuda(spectrum), 2 * n2, impl=impl),
+                           ref.irfft2(spectrum, (n1, 2 * n2)), 2 * n1 * n2, axes=AXES)
