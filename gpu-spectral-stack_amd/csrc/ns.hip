@@ -128,33 +128,38 @@ __device__ __forceinline__ void inverse_columns(const cf32* W, cf32* T, int whic
     }
 }
 
-// Real inverse of tile row `src` (m nonzero bins) for one row: prepare into the scratch row s,
-// M-point inverse transform; on return v holds the row's reals as complex pairs, in the last
-// stage's slots, scaled by `scale`.
+// Real inverse of tile row `src` (m nonzero bins) for one row: each lane forms the prepared values
+// of its own first-stage inputs straight from the tile row, Z[k] = ev + i d w^k with ev, d from
+// X[k] and conj(X[M-k]) and w = exp(i pi / M), then runs the M-point inverse transform (s is its
+// exchange scratch); on return v holds the row's reals as complex pairs, in the last stage's
+// slots, scaled by `scale`. A lane's inputs are k = lane + q L (q < E), so its twiddles are
+// w^lane times compile-time constants.
 template <class NP>
 __device__ __forceinline__ void row_c2r(const cf32* src, cf32* s, cf32 (&v)[NP::PR::E], int lane,
                                         float scale)
 {
     using PR = typename NP::PR;
     constexpr int M = NP::M;
-    for (int k = lane; k <= M / 2; k += PR::L) {
+    constexpr int R0 = PR::template radix<0>();
+    static_assert(M >= NP::m, "X[M] (Nyquist) lies outside the kept bins");
+    const cf32 base = twiddle_of<2 * M, true>(lane);
+    static_for<0, PR::E>([&](auto ei) {
+        constexpr int e = decltype(ei)::value;
+        constexpr int b = e / R0;
+        constexpr int r = e % R0;
+        constexpr int off = b * PR::L + r * (PR::N / R0);  // k = lane + off
+        const int k = lane + off;
         cf32 xk = k < NP::m ? src[k] : czero();
-        cf32 xm = M - k < NP::m ? src[M - k] : czero();
+        const cf32 xm = (k > 0 && M - k < NP::m) ? src[M - k] : czero();
         if (k == 0) {
             xk.im = 0.0f;
-            xm.im = 0.0f;
         }
         const cf32 ev{0.5f * (xk.re + xm.re), 0.5f * (xk.im - xm.im)};
         const cf32 d{0.5f * (xk.re - xm.re), 0.5f * (xk.im + xm.im)};
-        const cf32 od = cmul(d, twiddle_of<2 * M, true>(k));
-        const cf32 iod{-od.im, od.re};
-        s[pad(k)] = cadd(ev, iod);
-        if (k > 0 && k < M - k) {
-            s[pad(M - k)] = cconj(csub(ev, iod));
-        }
-    }
-    lds_sync<true>();
-    stage_read<PR, 0>(s, v, lane);
+        constexpr cf32 c = const_twiddle<true>(off, 2 * M);
+        const cf32 od = cmul(d, off == 0 ? base : cmul(base, c));
+        v[e] = cf32{ev.re - od.im, ev.im + od.re};
+    });
     run_stages<PR, 0, true, false>(v, s, lane, nullptr);
 #pragma unroll
     for (int e = 0; e < PR::E; ++e) {
