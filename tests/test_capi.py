@@ -165,3 +165,92 @@ def test_direct_calls_on_an_explicit_stream(lib, rng):
     assert rc == SPX_OK, _last(lib)
     stream.synchronize()
     assert_transform_close(cd, ref.rfft(r), 2048)
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+@pytest.mark.gpu
+def test_direct_2d_and_modes_calls(lib, rng):
+    # Single-pass (128 x 128), column-first (512 x 512) and pruned paths through the C ABI itself,
+    # with the workspace the query asks for.
+    from oracle import reference as ref
+    from oracle.tolerance import assert_transform_close, random_complex, random_real
+
+    for n in (128, 512):
+        r = random_real(rng, (3, n, n))
+        rd = torch.from_numpy(r).cuda()
+        yd = torch.empty(3, n, n // 2 + 1, dtype=torch.complex64, device="cuda")
+        count = ctypes.c_size_t()
+        assert lib.spx_fft2_r2c_workspace(3, 1, n, n, 3, ctypes.byref(count)) == SPX_OK
+        work = torch.empty(max(count.value, 1), dtype=torch.complex64, device="cuda")
+        assert lib.spx_fft2_r2c(3, 1, _ptr(rd), _ptr(yd), n, n, 3, _ptr(work), None) == SPX_OK
+        assert lib.spx_fft2_c2r_workspace(3, 1, n, n, 3, ctypes.byref(count)) == SPX_OK
+        work2 = torch.empty(max(count.value, 1), dtype=torch.complex64, device="cuda")
+        back = torch.empty_like(rd)
+        assert lib.spx_fft2_c2r(3, 1, _ptr(yd), _ptr(back), n, n, 3, _ptr(work2), None) == SPX_OK
+        torch.cuda.synchronize()
+        assert_transform_close(yd, ref.rfft2(r), n * n, axes=(-2, -1))
+        assert_transform_close(back, r, n * n, axes=(-2, -1))
+
+    x = random_complex(rng, (5, 64, 64))
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.empty_like(xd)
+    assert lib.spx_fft2_c2c(3, 1, _ptr(xd), _ptr(yd), 64, 64, 5, 0, None, None) == SPX_OK
+    torch.cuda.synchronize()
+    assert_transform_close(yd, ref.fft2(x), 64 * 64, axes=(-2, -1))
+
+    r = random_real(rng, (4, 128, 128))
+    rd = torch.from_numpy(r).cuda()
+    md = torch.empty(4, 32, 16, dtype=torch.complex64, device="cuda")
+    assert lib.spx_rfft2_modes(3, _ptr(rd), _ptr(md), 128, 128, 16, 16, 4, None, None) == SPX_OK
+    out = torch.empty_like(rd)
+    assert lib.spx_irfft2_modes(3, _ptr(md), _ptr(out), 128, 128, 16, 16, 4, None, None) == SPX_OK
+    torch.cuda.synchronize()
+    modes = ref.rfft2_truncate(r, 16, 16)
+    assert_transform_close(md, modes, 128 * 128, axes=(-2, -1))
+    assert_transform_close(out, ref.irfft2_from_modes(modes, (128, 128)), 128 * 128,
+                           axes=(-2, -1))
+
+
+@pytest.mark.gpu
+def test_direct_radio_and_navier_stokes_calls(lib, rng):
+    import numpy as np
+    import scipy.signal
+
+    from oracle.tolerance import random_complex, random_real
+    from spectral.flow import Flow
+    from spectral.flow.gpu import GpuSolver
+
+    ll = ctypes.c_longlong
+    x = random_complex(rng, (2, 3000))
+    taps = random_real(rng, 63)
+    h = np.zeros(256, dtype=np.complex64)
+    h[:63] = taps
+    xd = torch.from_numpy(x).cuda()
+    hd = torch.from_numpy(np.fft.fft(h).astype(np.complex64)).cuda()
+    yd = torch.empty_like(xd)
+    assert lib.spx_rf_fir(3, _ptr(xd), _ptr(hd), _ptr(yd), ll(3000), 63, 256, ll(2), None) == SPX_OK
+    spec = torch.empty(2, 3, 1024, dtype=torch.complex64, device="cuda")
+    assert lib.spx_rf_spectrum(3, _ptr(xd), None, _ptr(spec), ll(3000), 1024, ll(2), None) == SPX_OK
+    torch.cuda.synchronize()
+    expected = scipy.signal.lfilter(taps.astype(np.float64), 1.0, x.astype(np.complex128))
+    assert np.linalg.norm(yd.cpu().numpy() - expected) / np.linalg.norm(expected) < 2e-5
+    padded = np.zeros((2, 3072), dtype=np.complex128)
+    padded[:, :3000] = x
+    frames = np.fft.fft(padded.reshape(2, 3, 1024), axis=-1)
+    assert np.linalg.norm(spec.cpu().numpy() - frames) / np.linalg.norm(frames) < 1e-5
+
+    # One predictor stage of 3 fields of 64^2 against the solver's own fused operator.
+    solver = GpuSolver(64, Flow(viscosity=np.array([1e-3, 2e-3, 3e-3])), 2.5e-3, pruned=True)
+    w = solver.to_spectral(torch.from_numpy(rng.standard_normal((3, 64, 64))).float().cuda())
+    f0 = torch.empty_like(w)
+    pred = torch.empty_like(w)
+    assert lib.spx_ns_stage(_ptr(w), None, None, _ptr(f0), _ptr(pred), _ptr(solver.forcing_hat),
+                            ctypes.c_void_p(solver.nu.data_ptr()), 1, ctypes.c_float(0.1),
+                            ctypes.c_float(2.5e-3), 64, 3, 0, None) == SPX_OK
+    ref_f0, ref_pred = torch.ops.spectral.ns_predict(w, solver.forcing_hat, solver.nu, 0.1,
+                                                     2.5e-3, 64)
+    torch.cuda.synchronize()
+    assert torch.equal(f0, ref_f0) and torch.equal(pred, ref_pred)
