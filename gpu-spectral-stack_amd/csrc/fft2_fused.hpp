@@ -159,7 +159,9 @@ __global__ void __launch_bounds__(F::NT)
         lds_sync<true>();
         final_write<PR>(s, v, lane);
         lds_sync<true>();
-        for (int k = lane; k <= F::M / 2; k += PR::L) {
+        // Pairs (k, M - k) up to M / 2; with w <= M / 2 kept columns only X[k], k < w, is read.
+        const int kmax = w > F::M / 2 ? F::M / 2 : w - 1;
+        for (int k = lane; k <= kmax; k += PR::L) {
             combine_row<F::M>(s, k);
         }
     }
