@@ -17,6 +17,10 @@
 //   inverse  the mirror: load the kept rows and columns (zero elsewhere), inverse columns, then per
 //            row the c2r prepare, an inverse n2/2-point transform, and the real row stored.
 //
+// When all n2/2 + 1 columns are kept, the DC and Nyquist columns (real in every row after the row
+// transforms) travel as one complex column and are split after the column pass (forward) or
+// joined before it (inverse), so n2/2 column transforms cover n2/2 + 1 columns.
+//
 // Normalization follows numpy: forward none, inverse 1 / (n1 n2) (the column and row scales are
 // folded into the row pass). The butterflies, twiddles and exchanges are the ones of stockham.hpp.
 
@@ -24,20 +28,18 @@
 
 namespace spx::dev {
 
-// floor(x / d) by a multiply-high with m = ceil(2^32 / d): exact for x, d < 2^16 (the error term
-// x (m d - 2^32) / 2^32 < x d / 2^32 < 1 never reaches the next integer).
+// floor(x / d) as one 32-bit multiply-high: m = ceil(2^31 / d) (2^31 at d = 1, so it fits), and
+// mulhi(2 x, m) = floor(x / d + x e / 2^31) with 0 <= e < 1. The fraction of x / d is at most
+// (d - 1) / d, so the quotient is exact whenever x e / 2^31 < 1 / d, i.e. whenever x d < 2^31.
 struct FastDiv {
     unsigned d;
-    unsigned long long m;
+    unsigned m;
 
     static FastDiv of(unsigned d)
     {
-        return {d, ((1ULL << 32) + d - 1) / d};
+        return {d, static_cast<unsigned>(((1ULL << 31) + d - 1) / d)};
     }
-    __device__ __forceinline__ unsigned div(unsigned x) const
-    {
-        return static_cast<unsigned>((static_cast<unsigned long long>(x) * m) >> 32);
-    }
+    __device__ __forceinline__ unsigned div(unsigned x) const { return __umulhi(x << 1, m); }
 };
 
 template <int N1_, int M_, int R, bool Table, int BudgetKB = 80>
@@ -69,6 +71,9 @@ struct Fused2d {
     static_assert(PR::L <= 64 && PC::L <= 64, "row and column transforms stay inside a wave");
     static_assert(kRows % RPP == 0, "row passes cover the rows exactly");
     static_assert(AP * kTile * sizeof(cf32) <= BudgetKB * 1024, "tile exceeds the LDS budget");
+    // Flat indices stay below AP N1 (M + 1) and divisors at most N1 (M + 1): FastDiv is exact.
+    static_assert(static_cast<long long>(AP) * N1 * (M + 1) * N1 * (M + 1) < (1LL << 31),
+                  "FastDiv range");
 
     // Tile row holding frequency-row f of the kept rows (all rows when m1 = 0).
     __device__ __forceinline__ static int row_of(int f, int m1)
@@ -77,43 +82,158 @@ struct Fused2d {
     }
 };
 
-// Combine of the real forward transform for one row held in place at s (Padded): pair k reads
-// Z[k] and Z[M-k] and writes X[k] and X[M-k] into the same slots (X[M] into slot M for k = 0).
+// Combine of the real forward transform for one row held in place at s (Padded): pair k (0 < k
+// <= M / 2) reads Z[k] and Z[M-k] and writes X[k] and X[M-k] into the same slots; tw =
+// exp(-pi i k / M). k = 0 gives the two real bins X[0] and X[M]: with pack, both go to slot 0 as
+// X[0] + i X[M] (the packed DC / Nyquist column), else X[0] alone (X[M] is not kept).
 template <int M>
-__device__ __forceinline__ void combine_row(cf32* s, int k)
+__device__ __forceinline__ void combine_pair(cf32* s, int k, cf32 tw, bool pack)
 {
-    const cf32 zk = s[pad(k & (M - 1))];
-    const cf32 zm = s[pad((M - k) & (M - 1))];
+    if (k == 0) {
+        const cf32 z0 = s[0];
+        s[0] = cf32{z0.re + z0.im, pack ? z0.re - z0.im : 0.0f};
+        return;
+    }
+    const cf32 zk = s[pad(k)];
+    const cf32 zm = s[pad(M - k)];
     const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
     const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
-    const cf32 wo = cmul(twiddle_of<2 * M, false>(k), od);
+    const cf32 wo = cmul(tw, od);
     s[pad(k)] = cadd(ev, wo);
     if (k < M - k) {
         s[pad(M - k)] = cconj(csub(ev, wo));
     }
 }
 
-// Prepare of the real inverse transform for one row in place at s (Padded): X[k] for k < w, zero
-// beyond; imaginary parts of X[0] and X[M] dropped.
-template <int M>
-__device__ __forceinline__ void prepare_row(cf32* s, int k, int w)
+// The combines of one row's pairs k = lane + j L <= kmax (L lanes per row). A lane evaluates one
+// twiddle, exp(-pi i lane / M), and reaches its other pairs' through compile-time constants.
+template <int M, int L>
+__device__ __forceinline__ void combine_row(cf32* s, int lane, int kmax, bool pack)
 {
-    cf32 xk = k < w ? s[pad(k)] : czero();
-    cf32 xm = M - k < w ? s[pad(M - k)] : czero();
+    const cf32 base = twiddle_of<2 * M, false>(lane);
+    static_for<0, M / 2 / L + 1>([&](auto ji) {
+        constexpr int j = decltype(ji)::value;
+        const int k = lane + j * L;
+        if (k <= kmax) {
+            if constexpr (j == 0) {
+                combine_pair<M>(s, k, base, pack);
+            } else {
+                constexpr cf32 c = const_twiddle<false>(j * L, 2 * M);
+                combine_pair<M>(s, k, cmul(base, c), pack);
+            }
+        }
+    });
+}
+
+// Prepare of the real inverse transform for one row in place at s (Padded): X[k] for k < w, zero
+// beyond; imaginary parts of X[0] and X[M] dropped. With pack, slot 0 holds X[0] + i X[M] (both
+// already real). tw = exp(pi i k / M).
+template <int M>
+__device__ __forceinline__ void prepare_pair(cf32* s, int k, int w, cf32 tw, bool pack)
+{
+    cf32 xk;
+    cf32 xm;
     if (k == 0) {
-        xk.im = 0.0f;
-        xm.im = 0.0f;
+        const cf32 p = s[0];
+        xk = cf32{p.re, 0.0f};
+        xm = cf32{pack ? p.im : 0.0f, 0.0f};
+    } else {
+        xk = k < w ? s[pad(k)] : czero();
+        xm = M - k < w ? s[pad(M - k)] : czero();
     }
     const cf32 ev{0.5f * (xk.re + xm.re), 0.5f * (xk.im - xm.im)};
     const cf32 d{0.5f * (xk.re - xm.re), 0.5f * (xk.im + xm.im)};
-    const cf32 od = cmul(d, twiddle_of<2 * M, true>(k));
+    const cf32 od = cmul(d, tw);
     const cf32 iod{-od.im, od.re};
-    if (k < M) {
-        s[pad(k)] = cadd(ev, iod);
-    }
+    s[pad(k)] = cadd(ev, iod);
     if (k > 0 && k < M - k) {
         s[pad(M - k)] = cconj(csub(ev, iod));
     }
+}
+
+template <int M, int L>
+__device__ __forceinline__ void prepare_row(cf32* s, int lane, int w, bool pack)
+{
+    const cf32 base = twiddle_of<2 * M, true>(lane);
+    static_for<0, M / 2 / L + 1>([&](auto ji) {
+        constexpr int j = decltype(ji)::value;
+        const int k = lane + j * L;
+        if (k <= M / 2) {
+            if constexpr (j == 0) {
+                prepare_pair<M>(s, k, w, base, pack);
+            } else {
+                constexpr cf32 c = const_twiddle<true>(j * L, 2 * M);
+                prepare_pair<M>(s, k, w, cmul(base, c), pack);
+            }
+        }
+    });
+}
+
+// Columns 0 and M of a forward tile from the packed column P = C0 + i CM, where C0 and CM are the
+// transforms of the real columns X[., 0] and X[., M] and so Hermitian: C0 = (P + conj P[-k]) / 2
+// and CM = (P - conj P[-k]) / 2i. Task (array, k1), k1 = 0 .. N1 / 2, owns rows k1 and -k1.
+template <class F>
+__device__ __forceinline__ void unpack_dc_nyquist(cf32* tile, int tid)
+{
+    constexpr int H = F::N1 / 2 + 1;
+    for (int e = tid; e < F::AP * H; e += F::NT) {
+        const int a = e / H;
+        const int k1 = e - a * H;
+        const int k2 = (F::N1 - k1) & (F::N1 - 1);
+        cf32* const t = tile + a * F::kTile;
+        const cf32 p = t[k1 * F::TS];
+        const cf32 q = t[k2 * F::TS];
+        const cf32 c0{0.5f * (p.re + q.re), 0.5f * (p.im - q.im)};
+        const cf32 cm{0.5f * (p.im + q.im), -0.5f * (p.re - q.re)};
+        t[k1 * F::TS] = c0;
+        t[k1 * F::TS + pad(F::M)] = cm;
+        t[k2 * F::TS] = cconj(c0);
+        t[k2 * F::TS + pad(F::M)] = cconj(cm);
+    }
+}
+
+// The inverse's mirror: columns 0 and M of the loaded spectrum into one column P = H0 + i HM,
+// where H = (c + conj c[-k]) / 2 is the Hermitian part of a column, whose inverse transform is
+// the real part of the column's (what the row inverse keeps of the DC and Nyquist bins). With
+// m1 > 0 the kept rows are 0 .. m1-1 and N1-m1 .. N1-1, so row -m1 is kept and its mirror m1 is
+// not: dropped rows are read as zeros here, P is written to row m1 too, and the packed column's
+// load reads rows 0 .. m1 (packed_kept).
+template <class F>
+__device__ __forceinline__ bool kept_row(int i, int m1)
+{
+    return m1 == 0 || i < m1 || i >= F::N1 - m1;
+}
+
+template <class F>
+__device__ __forceinline__ void pack_dc_nyquist(cf32* tile, int m1, int tid)
+{
+    constexpr int H = F::N1 / 2 + 1;
+    for (int e = tid; e < F::AP * H; e += F::NT) {
+        const int a = e / H;
+        const int k1 = e - a * H;
+        const int k2 = (F::N1 - k1) & (F::N1 - 1);
+        const bool kept1 = kept_row<F>(k1, m1);
+        const bool kept2 = kept_row<F>(k2, m1);
+        if (!kept1 && !kept2) {
+            continue;
+        }
+        cf32* const t = tile + a * F::kTile;
+        const cf32 a0 = kept1 ? t[k1 * F::TS] : czero();
+        const cf32 b0 = kept2 ? t[k2 * F::TS] : czero();
+        const cf32 am = kept1 ? t[k1 * F::TS + pad(F::M)] : czero();
+        const cf32 bm = kept2 ? t[k2 * F::TS + pad(F::M)] : czero();
+        const cf32 h0{0.5f * (a0.re + b0.re), 0.5f * (a0.im - b0.im)};
+        const cf32 hm{0.5f * (am.re + bm.re), 0.5f * (am.im - bm.im)};
+        t[k1 * F::TS] = cf32{h0.re - hm.im, h0.im + hm.re};
+        t[k2 * F::TS] = cf32{h0.re + hm.im, hm.re - h0.im};
+    }
+}
+
+// Rows of column c read from the tile by the inverse column pass; the others are zeros.
+template <class F>
+__device__ __forceinline__ bool packed_kept(int i, int m1, bool packed_column)
+{
+    return kept_row<F>(i, m1) || (packed_column && i == m1);
 }
 
 // Forward: z = the real arrays viewed as complex (batch x N1 x M), y = batch arrays of rows_out x w
@@ -130,6 +250,10 @@ __global__ void __launch_bounds__(F::NT)
     const long long first = static_cast<long long>(blockIdx.x) * F::AP;
     const int count = static_cast<int>(batch - first < F::AP ? batch - first : F::AP);
     const int tid = threadIdx.x;
+    // All M + 1 columns kept: the real DC and Nyquist columns travel as one complex column, so
+    // M column transforms (one pass at 128 x 128) cover M + 1 columns.
+    const bool pack = w == F::M + 1;
+    const int ncols = pack ? F::M : w;
 
     // Rows: load straight from HBM, transform, combine in place. (Staging short rows flat through
     // the tile first, as the complex kernel does, measured 10-20 % slower here.)
@@ -160,22 +284,19 @@ __global__ void __launch_bounds__(F::NT)
         final_write<PR>(s, v, lane);
         lds_sync<true>();
         // Pairs (k, M - k) up to M / 2; with w <= M / 2 kept columns only X[k], k < w, is read.
-        const int kmax = w > F::M / 2 ? F::M / 2 : w - 1;
-        for (int k = lane; k <= kmax; k += PR::L) {
-            combine_row<F::M>(s, k);
-        }
+        combine_row<F::M, PR::L>(s, lane, w > F::M / 2 ? F::M / 2 : w - 1, pack);
     }
     __syncthreads();
 
-    // Columns 0 .. w-1 of every array, in place down the tile.
-    const int total_cols = F::AP * w;
+    // Columns 0 .. ncols-1 of every array, in place down the tile.
+    const int total_cols = F::AP * ncols;
 #pragma unroll 1
     for (int c0 = 0; c0 < total_cols; c0 += F::CPP) {
         const int cg = c0 + tid / PC::L;
         const int lane = tid % PC::L;
         if (cg < total_cols) {
-            const int a = static_cast<int>(wdiv.div(static_cast<unsigned>(cg)));
-            const int c = cg - a * w;
+            const int a = pack ? cg / F::M : static_cast<int>(wdiv.div(static_cast<unsigned>(cg)));
+            const int c = cg - a * ncols;
             cf32* const s = tile + a * F::kTile + pad(c);
             cf32 v[PC::E];
             stage_read<PC, 0, Strided<F::TS>>(s, v, lane);
@@ -185,11 +306,16 @@ __global__ void __launch_bounds__(F::NT)
         }
     }
     __syncthreads();
+    if (pack) {
+        unpack_dc_nyquist<F>(tile, tid);
+        __syncthreads();
+    }
 
     // Store the kept rows of the first w columns. The workgroup's output is one contiguous run of
     // count x rows_out x w values: the lanes walk it flat, coalesced whatever w is (rows of a
     // few values, as at 4 x 4, would otherwise leave most of a wave idle), reading kStoreChunk
-    // tile values into registers before storing them.
+    // tile values into registers before storing them. The reads are unconditional (lanes past
+    // the end read the last value again), so they issue back to back.
     const int per_array = (m1 > 0 ? 2 * m1 : F::N1) * w;
     const int total = count * per_array;
     cf32* const dst = y + first * per_array;
@@ -199,13 +325,11 @@ __global__ void __launch_bounds__(F::NT)
         cf32 val[kStoreChunk];
 #pragma unroll
         for (int k = 0; k < kStoreChunk; ++k) {
-            const int e = e0 + k * F::NT + tid;
-            if (e < total) {
-                const int a = static_cast<int>(odiv.div(static_cast<unsigned>(e)));
-                const int r = e - a * per_array;
-                const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(r)));
-                val[k] = tile[a * F::kTile + F::row_of(f, m1) * F::TS + pad(r - f * w)];
-            }
+            const int e = cmin(e0 + k * F::NT + tid, total - 1);
+            const int a = F::AP == 1 ? 0 : static_cast<int>(odiv.div(static_cast<unsigned>(e)));
+            const int r = e - a * per_array;
+            const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(r)));
+            val[k] = tile[a * F::kTile + F::row_of(f, m1) * F::TS + pad(r - f * w)];
         }
 #pragma unroll
         for (int k = 0; k < kStoreChunk; ++k) {
@@ -233,8 +357,11 @@ __global__ void __launch_bounds__(F::NT)
     const int count = static_cast<int>(batch - first < F::AP ? batch - first : F::AP);
     const int tid = threadIdx.x;
 
+    const bool pack = w == F::M + 1;  // DC and Nyquist columns as one (see pack_dc_nyquist)
+    const int ncols = pack ? F::M : w;
+
     // Load the kept rows of the first w columns (contiguous in x: count arrays of rows_in x w),
-    // every lane's loads in flight before any LDS write; then zero the dropped rows.
+    // every lane's loads in flight before any LDS write.
     const int rows_in = m1 > 0 ? 2 * m1 : F::N1;
     const int per_array = rows_in * w;
     const int total = count * per_array;
@@ -249,7 +376,7 @@ __global__ void __launch_bounds__(F::NT)
     for (int k = 0; k < F::kMaxLoads; ++k) {
         const int e = tid + k * F::NT;
         if (e < total) {
-            const int a = static_cast<int>(adiv.div(static_cast<unsigned>(e)));
+            const int a = F::AP == 1 ? 0 : static_cast<int>(adiv.div(static_cast<unsigned>(e)));
             const int rem = e - a * per_array;
             const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(rem)));
             const int c = rem - f * w;
@@ -257,18 +384,22 @@ __global__ void __launch_bounds__(F::NT)
         }
     }
     __syncthreads();
+    if (pack) {
+        pack_dc_nyquist<F>(tile, m1, tid);
+        __syncthreads();
+    }
 
-    // Inverse columns 0 .. w-1, in place. The dropped rows (m1 > 0) are read as zeros, never
+    // Inverse columns 0 .. ncols-1, in place. The dropped rows (m1 > 0) are read as zeros, never
     // from the tile: the column's later stages overwrite all its rows anyway.
-    const int total_cols = F::AP * w;
+    const int total_cols = F::AP * ncols;
     constexpr int R0 = PC::template radix<0>();
 #pragma unroll 1
     for (int c0 = 0; c0 < total_cols; c0 += F::CPP) {
         const int cg = c0 + tid / PC::L;
         const int lane = tid % PC::L;
         if (cg < total_cols) {
-            const int a = static_cast<int>(wdiv.div(static_cast<unsigned>(cg)));
-            const int c = cg - a * w;
+            const int a = pack ? cg / F::M : static_cast<int>(wdiv.div(static_cast<unsigned>(cg)));
+            const int c = cg - a * ncols;
             cf32* const s = tile + a * F::kTile + pad(c);
             cf32 v[PC::E];
 #pragma unroll
@@ -276,7 +407,7 @@ __global__ void __launch_bounds__(F::NT)
 #pragma unroll
                 for (int r = 0; r < R0; ++r) {
                     const int i = input_index<PC, 0>(lane, b, r);
-                    const bool kept = m1 == 0 || i < m1 || i >= F::N1 - m1;
+                    const bool kept = packed_kept<F>(i, m1, pack && c == 0);
                     v[b * R0 + r] = kept ? s[i * F::TS] : czero();
                 }
             }
@@ -296,9 +427,7 @@ __global__ void __launch_bounds__(F::NT)
         const int lane = tid % PR::L;
         const int a = row / F::N1;
         cf32* const s = tile + a * F::kTile + (row % F::N1) * F::TS;
-        for (int k = lane; k <= F::M / 2; k += PR::L) {
-            prepare_row<F::M>(s, k, w);
-        }
+        prepare_row<F::M, PR::L>(s, lane, w, pack);
         lds_sync<true>();
         cf32 v[PR::E];
         stage_read<PR, 0>(s, v, lane);
