@@ -255,37 +255,44 @@ __global__ void __launch_bounds__(F::NT)
     const bool pack = w == F::M + 1;
     const int ncols = pack ? F::M : w;
 
-    // Rows: load straight from HBM, transform, combine in place. (Staging short rows flat through
-    // the tile first, as the complex kernel does, measured 10-20 % slower here.)
-#pragma unroll 1
-    for (int p = 0; p < F::kRows / F::RPP; ++p) {
-        const int row = p * F::RPP + tid / PR::L;  // row of the workgroup's arrays
-        const int lane = tid % PR::L;
-        const int a = row / F::N1;
-        cf32* const s = tile + a * F::kTile + (row % F::N1) * F::TS;
-        cf32 v[PR::E];
-        if (a < count) {
-            const cf32* src = z + (first * F::N1 + row) * F::M;
+    // Rows: load straight from HBM, transform, combine in place. Every pass's loads are issued
+    // before the first pass's transform, so later passes' loads arrive during earlier passes'
+    // work. (Staging short rows flat through the tile first, as the complex kernel does,
+    // measured 10-20 % slower here.)
+    constexpr int kPasses = F::kRows / F::RPP;
+    constexpr int R0 = PR::template radix<0>();
+    static_assert(kPasses * PR::E <= 32, "all row passes' inputs fit in registers");
+    const int lane = tid % PR::L;
+    cf32 v[kPasses][PR::E];
+    static_for<0, kPasses>([&](auto pi) {
+        constexpr int p = decltype(pi)::value;
+        // Row of the workgroup's arrays; rows of arrays past the batch read the last array's
+        // (their tile rows are never stored), so every load is unconditional.
+        const int row = p * F::RPP + tid / PR::L;
+        const int a = cmin(row / F::N1, count - 1);
+        const cf32* src = z + (first * F::N1 + a * F::N1 + row % F::N1) * F::M;
 #pragma unroll
-            for (int b = 0; b < PR::E / PR::template radix<0>(); ++b) {
+        for (int b = 0; b < PR::E / R0; ++b) {
 #pragma unroll
-                for (int r = 0; r < PR::template radix<0>(); ++r) {
-                    v[b * PR::template radix<0>() + r] = src[input_index<PR, 0>(lane, b, r)];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < PR::E; ++e) {
-                v[e] = czero();
+            for (int r = 0; r < R0; ++r) {
+                v[p][b * R0 + r] = src[input_index<PR, 0>(lane, b, r)];
             }
         }
-        run_stages<PR, 0, false, F::kTable>(v, s, lane, table);
+        // Keep the passes' loads in pass order, so pass 0's transform waits for its own loads
+        // only (the memory counter retires loads in issue order).
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    static_for<0, kPasses>([&](auto pi) {
+        constexpr int p = decltype(pi)::value;
+        const int row = p * F::RPP + tid / PR::L;
+        cf32* const s = tile + (row / F::N1) * F::kTile + (row % F::N1) * F::TS;
+        run_stages<PR, 0, false, F::kTable>(v[p], s, lane, table);
         lds_sync<true>();
-        final_write<PR>(s, v, lane);
+        final_write<PR>(s, v[p], lane);
         lds_sync<true>();
         // Pairs (k, M - k) up to M / 2; with w <= M / 2 kept columns only X[k], k < w, is read.
         combine_row<F::M, PR::L>(s, lane, w > F::M / 2 ? F::M / 2 : w - 1, pack);
-    }
+    });
     __syncthreads();
 
     // Columns 0 .. ncols-1 of every array, in place down the tile.
@@ -366,16 +373,20 @@ __global__ void __launch_bounds__(F::NT)
     const int per_array = rows_in * w;
     const int total = count * per_array;
     const cf32* const src = x + first * per_array;
+    // Steps past the end are skipped whole (a test uniform over the workgroup); within the last
+    // step, lanes past the end load and write the last value again (same value, same slot), so
+    // no load or LDS write waits on a per-lane branch.
     cf32 val[F::kMaxLoads];
 #pragma unroll
     for (int k = 0; k < F::kMaxLoads; ++k) {
-        const int e = tid + k * F::NT;
-        val[k] = e < total ? src[e] : czero();
+        if (k * F::NT < total) {
+            val[k] = src[cmin(tid + k * F::NT, total - 1)];
+        }
     }
 #pragma unroll
     for (int k = 0; k < F::kMaxLoads; ++k) {
-        const int e = tid + k * F::NT;
-        if (e < total) {
+        if (k * F::NT < total) {
+            const int e = cmin(tid + k * F::NT, total - 1);
             const int a = F::AP == 1 ? 0 : static_cast<int>(adiv.div(static_cast<unsigned>(e)));
             const int rem = e - a * per_array;
             const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(rem)));
@@ -402,13 +413,17 @@ __global__ void __launch_bounds__(F::NT)
             const int c = cg - a * ncols;
             cf32* const s = tile + a * F::kTile + pad(c);
             cf32 v[PC::E];
+            if (m1 == 0) {
+                stage_read<PC, 0, Strided<F::TS>>(s, v, lane);
+            } else {
 #pragma unroll
-            for (int b = 0; b < PC::E / R0; ++b) {
+                for (int b = 0; b < PC::E / R0; ++b) {
 #pragma unroll
-                for (int r = 0; r < R0; ++r) {
-                    const int i = input_index<PC, 0>(lane, b, r);
-                    const bool kept = packed_kept<F>(i, m1, pack && c == 0);
-                    v[b * R0 + r] = kept ? s[i * F::TS] : czero();
+                    for (int r = 0; r < R0; ++r) {
+                        const int i = input_index<PC, 0>(lane, b, r);
+                        const bool kept = packed_kept<F>(i, m1, pack && c == 0);
+                        v[b * R0 + r] = kept ? s[i * F::TS] : czero();
+                    }
                 }
             }
             run_stages<PC, 0, true, F::kTable, Strided<F::TS>>(v, s, lane, table);
