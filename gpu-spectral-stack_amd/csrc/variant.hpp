@@ -8,6 +8,7 @@
 // real.cu:160-180, fourstep.cuh:110-131): callers and tests match on them.
 
 #include "fft2_fused.hpp"
+#include "fft2_modes.hpp"
 #include "fft2_pairs.hpp"
 #include "fft_api.hpp"
 #include "rf.hpp"
@@ -679,6 +680,19 @@ struct Stockham {
     X(4, 4) X(8, 8) X(16, 16) X(32, 32) X(32, 64) X(64, 32) X(64, 64) X(64, 128) X(128, 64)      \
     X(128, 128)
 
+// The fused shapes whose pruned transforms with w <= n2/8 kept columns take the narrow-tile
+// kernels of fft2_modes.hpp (n2 >= 64, and n1 at least one row pass, at most 128 rows).
+#define SPX_MODES_SHAPES(X)                                                                     \
+    X(64, 64) X(128, 64) X(32, 128) X(64, 128) X(128, 128) X(32, 256) X(64, 256)
+
+template <int N1, int N2>
+constexpr bool modes_shape()
+{
+#define SPX_X(A, B) || (N1 == (A) && N2 == (B))
+    return false SPX_MODES_SHAPES(SPX_X);
+#undef SPX_X
+}
+
 // Single-pass 2D drivers of one variant (radix 4 and up; radix 2 has none).
 template <int R, bool Table>
 struct Fused2dDriver {
@@ -721,6 +735,17 @@ struct Fused2dDriver {
     template <int N1, int M>
     static void launch_r2c(const float* x, cf32* y, int m1, int w, int batch, hipStream_t stream)
     {
+        if constexpr (modes_shape<N1, 2 * M>()) {
+            if (m1 > 0 && w <= M / 4) {
+                using F = dev::Modes2d<N1, M, R, Table>;
+                hipLaunchKernelGGL((dev::rfft2_modes_kernel<F>), dim3(static_cast<unsigned>(batch)),
+                                   dim3(F::NT), 0, stream, reinterpret_cast<const cf32*>(x), y, m1,
+                                   w, dev::FastDiv::of(static_cast<unsigned>(w)),
+                                   Table ? twiddle_table() : nullptr);
+                SPX_LAUNCH_CHECK();
+                return;
+            }
+        }
         using F = dev::Fused2d<N1, M, R, Table>;
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
         const cf32* table = Table ? twiddle_table() : nullptr;
@@ -736,6 +761,18 @@ struct Fused2dDriver {
     template <int N1, int M>
     static void launch_c2r(const cf32* x, float* y, int m1, int w, int batch, hipStream_t stream)
     {
+        if constexpr (modes_shape<N1, 2 * M>()) {
+            if (m1 > 0 && w <= M / 4) {
+                using F = dev::Modes2d<N1, M, R, Table>;
+                hipLaunchKernelGGL((dev::irfft2_modes_kernel<F>),
+                                   dim3(static_cast<unsigned>(batch)), dim3(F::NT), 0, stream, x,
+                                   reinterpret_cast<cf32*>(y), m1, w,
+                                   dev::FastDiv::of(static_cast<unsigned>(w)),
+                                   Table ? twiddle_table() : nullptr);
+                SPX_LAUNCH_CHECK();
+                return;
+            }
+        }
         using F = dev::Fused2d<N1, M, R, Table>;
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
         const cf32* table = Table ? twiddle_table() : nullptr;

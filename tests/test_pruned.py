@@ -180,3 +180,26 @@ def test_single_pass_modes_round_trip(rng, impl, n1, n2):
     given = random_complex(rng, (17, 2 * m1, m2))
     y = spectral.irfft2_from_modes(cuda(given), (n1, n2), impl=impl)
     assert_transform_close(y, ref.irfft2_from_modes(given, (n1, n2)), n1 * n2, axes=AXES)
+
+
+# Shapes whose pruned transforms with m2 <= n2/8 take the narrow-tile kernels (one array per
+# workgroup, only the kept columns in LDS); the edges of that path: one and n1/2 kept row pairs,
+# one and n2/8 kept columns, and n2/8 + 1 (the first width past it, back on the general kernel).
+NARROW_SHAPES = [(64, 64), (128, 64), (32, 128), (64, 128), (128, 128), (32, 256), (64, 256)]
+
+
+@pytest.mark.parametrize("impl", ["stockham_r4", "stockham_r8", "stockham_r8_table"])
+@pytest.mark.parametrize(("n1", "n2"), NARROW_SHAPES)
+@pytest.mark.parametrize(("m1_of", "m2_of"), [(lambda n: 1, lambda n: 1),
+                                              (lambda n: n // 2, lambda n: n // 8),
+                                              (lambda n: 1, lambda n: n // 8),
+                                              (lambda n: n // 4, lambda n: n // 8 + 1)])
+def test_narrow_modes_match_the_oracle(rng, impl, n1, n2, m1_of, m2_of):
+    m1, m2 = m1_of(n1), m2_of(n2)
+    x = random_real(rng, (5, n1, n2))
+    modes = spectral.rfft2_truncated(cuda(x), m1, m2, impl=impl)
+    assert modes.shape == (5, 2 * m1, m2)
+    assert_transform_close(modes, ref.rfft2_truncate(x, m1, m2), n1 * n2, axes=AXES)
+    given = random_complex(rng, (5, 2 * m1, m2))
+    y = spectral.irfft2_from_modes(cuda(given), (n1, n2), impl=impl)
+    assert_transform_close(y, ref.irfft2_from_modes(given, (n1, n2)), n1 * n2, axes=AXES)
