@@ -127,9 +127,11 @@ __device__ __forceinline__ void combine_row(cf32* s, int lane, int kmax, bool pa
 
 // Prepare of the real inverse transform for one row in place at s (Padded): X[k] for k < w, zero
 // beyond; imaginary parts of X[0] and X[M] dropped. With pack, slot 0 holds X[0] + i X[M] (both
-// already real). tw = exp(pi i k / M).
+// already real). tw = exp(pi i k / M); half = 1/2 times the inverse's scale, which the (linear)
+// row transform then carries to its outputs.
 template <int M>
-__device__ __forceinline__ void prepare_pair(cf32* s, int k, int w, cf32 tw, bool pack)
+__device__ __forceinline__ void prepare_pair(cf32* s, int k, int w, cf32 tw, bool pack,
+                                             float half)
 {
     cf32 xk;
     cf32 xm;
@@ -141,8 +143,8 @@ __device__ __forceinline__ void prepare_pair(cf32* s, int k, int w, cf32 tw, boo
         xk = k < w ? s[pad(k)] : czero();
         xm = M - k < w ? s[pad(M - k)] : czero();
     }
-    const cf32 ev{0.5f * (xk.re + xm.re), 0.5f * (xk.im - xm.im)};
-    const cf32 d{0.5f * (xk.re - xm.re), 0.5f * (xk.im + xm.im)};
+    const cf32 ev{half * (xk.re + xm.re), half * (xk.im - xm.im)};
+    const cf32 d{half * (xk.re - xm.re), half * (xk.im + xm.im)};
     const cf32 od = cmul(d, tw);
     const cf32 iod{-od.im, od.re};
     s[pad(k)] = cadd(ev, iod);
@@ -152,7 +154,7 @@ __device__ __forceinline__ void prepare_pair(cf32* s, int k, int w, cf32 tw, boo
 }
 
 template <int M, int L>
-__device__ __forceinline__ void prepare_row(cf32* s, int lane, int w, bool pack)
+__device__ __forceinline__ void prepare_row(cf32* s, int lane, int w, bool pack, float half)
 {
     const cf32 base = twiddle_of<2 * M, true>(lane);
     static_for<0, M / 2 / L + 1>([&](auto ji) {
@@ -160,10 +162,10 @@ __device__ __forceinline__ void prepare_row(cf32* s, int lane, int w, bool pack)
         const int k = lane + j * L;
         if (k <= M / 2) {
             if constexpr (j == 0) {
-                prepare_pair<M>(s, k, w, base, pack);
+                prepare_pair<M>(s, k, w, base, pack, half);
             } else {
                 constexpr cf32 c = const_twiddle<true>(j * L, 2 * M);
-                prepare_pair<M>(s, k, w, cmul(base, c), pack);
+                prepare_pair<M>(s, k, w, cmul(base, c), pack, half);
             }
         }
     });
@@ -532,16 +534,17 @@ __global__ void __launch_bounds__(F::NT)
     }
     __syncthreads();
 
-    // Rows: prepare in place, inverse transform, store the real row (scale 1 / (N1 M) covers
-    // both passes: the prepare's halves make 1 / M the row inverse of numpy's irfft).
-    constexpr float scale = 1.0f / static_cast<float>(F::N1 * F::M);
+    // Rows: prepare in place, inverse transform, store the real row. The scale 1 / (N1 M)
+    // covers both passes (the prepare's halves make 1 / M the row inverse of numpy's irfft) and
+    // rides on those halves.
+    constexpr float half = 0.5f / static_cast<float>(F::N1 * F::M);
 #pragma unroll 1
     for (int p = 0; p < F::kRows / F::RPP; ++p) {
         const int row = p * F::RPP + tid / PR::L;
         const int lane = tid % PR::L;
         const int a = row / F::N1;
         cf32* const s = tile + a * F::kTile + (row % F::N1) * F::TS;
-        prepare_row<F::M, PR::L>(s, lane, w, pack);
+        prepare_row<F::M, PR::L>(s, lane, w, pack, half);
         lds_sync<true>();
         cf32 v[PR::E];
         stage_read<PR, 0>(s, v, lane);
@@ -555,8 +558,7 @@ __global__ void __launch_bounds__(F::NT)
                 for (int b = 0; b < PR::E / RL; ++b) {
 #pragma unroll
                     for (int r = 0; r < RL; ++r) {
-                        st_stream(dst + lane + b * PR::L + r * (PR::N / RL),
-                                  cscale(v[b * RL + r], scale));
+                        st_stream(dst + lane + b * PR::L + r * (PR::N / RL), v[b * RL + r]);
                     }
                 }
             }
@@ -575,7 +577,7 @@ __global__ void __launch_bounds__(F::NT)
                 const int aw = rw / F::N1;
                 if (aw < count) {
                     st_stream(z + (first * F::N1 + rw) * F::M + i,
-                              cscale(tile[aw * F::kTile + (rw % F::N1) * F::TS + pad(i)], scale));
+                              tile[aw * F::kTile + (rw % F::N1) * F::TS + pad(i)]);
                 }
             }
         }

@@ -199,9 +199,11 @@ __global__ void __launch_bounds__(F::NT)
 
     // Rows. Lane slot k (k = lane + off) takes Z[k] = E + i O, E = (X[k] + conj X[M-k]) / 2,
     // O = exp(pi i k / M) (X[k] - conj X[M-k]) / 2, from the tile row (X[k] = 0 for k >= w; the
-    // imaginary part of X[0] dropped; X[M] is never kept, w < M). The scale 1 / (N1 M) covers
-    // both passes: the halves make 1 / M the row inverse of numpy's irfft.
-    constexpr float scale = 1.0f / static_cast<float>(F::N1 * F::M);
+    // imaginary part of X[0] dropped; X[M] is never kept, w < M). The scale 1 / (N1 M), which
+    // with the halves makes the row inverse numpy's irfft and covers both passes, rides on the
+    // halves. A slot whose k lies in [w, M - w] for every lane of the row is zero (a test
+    // uniform over the workgroup).
+    constexpr float half = 0.5f / static_cast<float>(F::N1 * F::M);
     constexpr int R0 = PR::template radix<0>();
     const int lane = tid % PR::L;
     const int prow = tid / PR::L;
@@ -216,14 +218,18 @@ __global__ void __launch_bounds__(F::NT)
         static_for<0, PR::E>([&](auto ei) {
             constexpr int e = decltype(ei)::value;
             constexpr int off = (e / R0) * PR::L + (e % R0) * (PR::N / R0);
+            if (off >= w && F::M - off - (PR::L - 1) >= w) {
+                v[e] = czero();
+                return;
+            }
             const int k = lane + off;
             cf32 xk = k < w ? trow[k] : czero();
             const cf32 xm = (k > 0 && F::M - k < w) ? trow[F::M - k] : czero();
             if (k == 0) {
                 xk.im = 0.0f;
             }
-            const cf32 ev{0.5f * (xk.re + xm.re), 0.5f * (xk.im - xm.im)};
-            const cf32 d{0.5f * (xk.re - xm.re), 0.5f * (xk.im + xm.im)};
+            const cf32 ev{half * (xk.re + xm.re), half * (xk.im - xm.im)};
+            const cf32 d{half * (xk.re - xm.re), half * (xk.im + xm.im)};
             constexpr cf32 c = const_twiddle<true>(off, 2 * F::M);
             const cf32 od = cmul(d, off == 0 ? base : cmul(base, c));
             v[e] = cf32{ev.re - od.im, ev.im + od.re};
@@ -237,8 +243,7 @@ __global__ void __launch_bounds__(F::NT)
             for (int b = 0; b < PR::E / RL; ++b) {
 #pragma unroll
                 for (int r = 0; r < RL; ++r) {
-                    st_stream(dst + lane + b * PR::L + r * (PR::N / RL),
-                              cscale(v[b * RL + r], scale));
+                    st_stream(dst + lane + b * PR::L + r * (PR::N / RL), v[b * RL + r]);
                 }
             }
             lds_sync<true>();  // the scratch is read before the next pass reuses it
@@ -254,8 +259,7 @@ __global__ void __launch_bounds__(F::NT)
 #pragma unroll
             for (int k = 0; k < PR::E; ++k) {
                 const int e = tid % 64 + k * 64;
-                st_stream(dst + e,
-                          cscale(lds[(r0 + e / F::M) * F::TR + pad(e % F::M)], scale));
+                st_stream(dst + e, lds[(r0 + e / F::M) * F::TR + pad(e % F::M)]);
             }
             lds_sync<true>();
         }
