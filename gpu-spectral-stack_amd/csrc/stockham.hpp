@@ -661,6 +661,14 @@ struct HasStage0 : std::false_type {};
 template <class Io>
 struct HasStage0<Io, std::void_t<decltype(Io::kStage0)>> : std::bool_constant<Io::kStage0> {};
 
+// An I/O policy with `static constexpr bool kFinal = true` takes the last stage's outputs from
+// registers itself (final<P, WaveLocal>(s, v, lane)) and leaves in LDS what its staged store
+// reads, instead of final_write.
+template <class Io, class = void>
+struct HasFinal : std::false_type {};
+template <class Io>
+struct HasFinal<Io, std::void_t<decltype(Io::kFinal)>> : std::bool_constant<Io::kFinal> {};
+
 template <class P, bool Inv, bool Table, class Io>
 __global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch, const cf32* table)
 {
@@ -729,9 +737,13 @@ __global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch
             }
         }
     } else {
-        lds_sync<kWaveGroups>();
-        final_write<P>(s, v, lane);
-        lds_sync<kWaveGroups>();
+        if constexpr (HasFinal<Io>::value) {
+            io.template final<P, kWaveGroups>(s, v, lane);
+        } else {
+            lds_sync<kWaveGroups>();
+            final_write<P>(s, v, lane);
+            lds_sync<kWaveGroups>();
+        }
         if (group_count == kGroupT) {
             io.template store<P, Full>(group_lds, group_first, kGroupT, gtid);
         } else {
@@ -821,9 +833,15 @@ struct C2cIo {
 // keep: values per row of y, m + 1 for the whole half spectrum, fewer when pruned.
 struct R2cIo {
     static constexpr bool kGroupIsBlock = false;
+    static constexpr bool kFinal = true;
     const cf32* z;  // x viewed as complex
     cf32* y;
     int keep;
+
+    // The combine done by the transform's own lanes from their registers (final) for m = 8 ..
+    // 64, a separate pass over the pairs otherwise.
+    template <class P>
+    static constexpr bool direct_combine() { return P::N >= 8 && P::N <= 64; }
 
     template <class P>
     static constexpr bool direct_in() { return P::L >= 16; }
@@ -851,30 +869,70 @@ struct R2cIo {
         });
     }
 
+    // Output slot e of the last stage holds Z[k], k = lane + off. With the row's Z in LDS, the
+    // lane reads Z[m-k] and forms X[k] = E + exp(-pi i k / m) O, E = (Z[k] + conj Z[m-k]) / 2,
+    // O = (Z[k] - conj Z[m-k]) / 2i (indices mod m), and X[m] = E[0] - O[0] at k = 0; then X
+    // replaces Z in LDS. A lane's k are lane plus compile-time offsets: one twiddle per lane.
+    template <class P, bool WaveLocal>
+    __device__ __forceinline__ void final(cf32* s, cf32 (&v)[P::E], int lane) const
+    {
+        lds_sync<WaveLocal>();
+        final_write<P>(s, v, lane);
+        lds_sync<WaveLocal>();
+        if constexpr (direct_combine<P>()) {
+            constexpr int m = P::N;
+            constexpr int RL = P::template radix<P::kStages - 1>();
+            const cf32 base = twiddle_of<2 * m, false>(lane);
+            cf32 xm{0.0f, 0.0f};
+            static_for<0, P::E>([&](auto ei) {
+                constexpr int e = decltype(ei)::value;
+                constexpr int off = (e / RL) * P::L + (e % RL) * (P::N / RL);
+                const int k = lane + off;
+                const cf32 zk = v[e];
+                const cf32 zm = s[pad((m - k) & (m - 1))];
+                const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
+                const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
+                constexpr cf32 c = const_twiddle<false>(off, 2 * m);
+                v[e] = cadd(ev, cmul(off == 0 ? base : cmul(base, c), od));
+                if constexpr (off == 0) {
+                    xm = csub(ev, od);  // X[m], kept by the lane with k = 0
+                }
+            });
+            lds_sync<WaveLocal>();  // every partner read is done before X replaces Z
+            final_write<P>(s, v, lane);
+            if (lane == 0) {
+                s[pad(m)] = xm;
+            }
+            lds_sync<WaveLocal>();
+        }
+    }
+
     template <class P, class G>
     __device__ __forceinline__ void store(cf32* lds, long long first, int count, int tid) const
     {
         constexpr int m = P::N;
-        // 1. Combine in place: pair k reads Z[k] and Z[m-k] and writes X[k] and X[m-k] to the
-        //    same two slots (k = 0 reads slot 0 and writes X[0] there and X[m] into slot m), so
-        //    no lane touches another lane's slots.
-        using S = Staged<G, m / 2 + 1>;
-        S::each(count, tid, [&](int, int u, int k, bool valid) {
-            if (!valid) {
-                return;
-            }
-            cf32* s = lds + u * P::kStride;
-            const cf32 zk = s[pad(k & (m - 1))];
-            const cf32 zm = s[pad((m - k) & (m - 1))];
-            const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
-            const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};  // (zk - conj zm)/2i
-            const cf32 wo = cmul(twiddle_of<2 * m, false>(k), od);  // exp(-pi i k / m) O
-            s[pad(k)] = cadd(ev, wo);
-            if (k < m - k) {
-                s[pad(m - k)] = cconj(csub(ev, wo));
-            }
-        });
-        lds_sync<G::kWave>();
+        if constexpr (!direct_combine<P>()) {
+            // 1. Combine in place: pair k reads Z[k] and Z[m-k] and writes X[k] and X[m-k] to the
+            //    same two slots (k = 0 reads slot 0 and writes X[0] there and X[m] into slot m),
+            //    so no lane touches another lane's slots.
+            using S = Staged<G, m / 2 + 1>;
+            S::each(count, tid, [&](int, int u, int k, bool valid) {
+                if (!valid) {
+                    return;
+                }
+                cf32* s = lds + u * P::kStride;
+                const cf32 zk = s[pad(k & (m - 1))];
+                const cf32 zm = s[pad((m - k) & (m - 1))];
+                const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
+                const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
+                const cf32 wo = cmul(twiddle_of<2 * m, false>(k), od);  // exp(-pi i k / m) O
+                s[pad(k)] = cadd(ev, wo);
+                if (k < m - k) {
+                    s[pad(m - k)] = cconj(csub(ev, wo));
+                }
+            });
+            lds_sync<G::kWave>();
+        }
         // 2. The first `keep` values of each row, stored contiguously.
         using H = Staged<G, m + 1>;
         cf32* dst = y + first * keep;
