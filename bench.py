@@ -88,26 +88,71 @@ def traffic_from_profiles(kernel_tag: str):
     return None
 
 
+def _host_cpu() -> str:
+    """The host CPU's model name, from /proc/cpuinfo (empty when unreadable)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _time_rows(fn, seconds: float) -> tuple[int, float]:
+    """Runs fn() (after one warm-up call) until `seconds` have passed: (calls, elapsed s)."""
+    fn()
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            return reps, elapsed
+
+
 def cpu_baseline(seconds: float) -> dict:
-    """numpy.fft forward + inverse over complex64 rows of 1024, timed on this host's cores."""
+    """numpy.fft forward + inverse over complex64 rows of 1024 on one host thread (the reported
+    value), then, in a quarter of that time each, the same work in complex128 on one thread and
+    scipy.fft complex64 on every host core. Rates use the complex64 work convention (16 B per
+    point per transform), so they compare directly with the GPU's."""
+    import os
+
     import numpy as np
 
     rng = np.random.default_rng(1)
     rows = 2048
     x = (rng.uniform(-1, 1, (rows, N)) + 1j * rng.uniform(-1, 1, (rows, N))).astype(np.complex64)
-    np.fft.ifft(np.fft.fft(x, axis=-1), axis=-1)  # warm-up
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        np.fft.ifft(np.fft.fft(x, axis=-1), axis=-1)
-        reps += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= seconds:
-            break
-    gbps = 2 * 16 * rows * N * reps / elapsed / 1e9
-    return {"value": round(gbps, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy {np.__version__} pocketfft fft+ifft complex64, {rows} x {N} rows "
-                      f"repeated {reps}x ({elapsed:.1f} s) on 1 host thread"}
+    work = 2 * 16 * rows * N  # bytes per forward + inverse pass
+
+    reps, elapsed = _time_rows(lambda: np.fft.ifft(np.fft.fft(x, axis=-1), axis=-1), seconds)
+    gbps = work * reps / elapsed / 1e9
+    out = {"value": round(gbps, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"numpy {np.__version__} pocketfft fft+ifft complex64, {rows} x {N} rows "
+                     f"repeated {reps}x ({elapsed:.1f} s) on 1 host thread"}
+
+    x64 = x.astype(np.complex128)
+    reps, elapsed = _time_rows(lambda: np.fft.ifft(np.fft.fft(x64, axis=-1), axis=-1),
+                               seconds / 4)
+    out["complex128_1_thread_gbps"] = round(work * reps / elapsed / 1e9, 3)
+    try:
+        import scipy
+        import scipy.fft
+
+        threads = os.cpu_count() or 1
+        reps, elapsed = _time_rows(
+            lambda: scipy.fft.ifft(scipy.fft.fft(x, axis=-1, workers=threads), axis=-1,
+                                   workers=threads),
+            seconds / 4)
+        out["scipy_all_cores_gbps"] = round(work * reps / elapsed / 1e9, 3)
+        out["scipy_threads"] = threads
+        out["scipy"] = scipy.__version__
+    except ImportError:
+        pass
+    out["host_cpu"] = _host_cpu()
+    return out
 
 
 def main(argv=None) -> int:

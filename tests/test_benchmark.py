@@ -105,3 +105,14 @@ def test_bench_torch_writes_one_row_per_size(tmp_path):
     assert bench_torch.main(["--sizes", "8,64", "--total", "4096", "--out", str(out)]) == 0
     rows = [line for line in out.read_text().splitlines() if line and not line.startswith("#")]
     assert len(rows) == 3 and rows[1].startswith("fft_c2c,torch,8,512,")
+
+
+def test_cpu_baseline_reports_its_sample_and_the_wider_rows():
+    import bench
+
+    cb = bench.cpu_baseline(0.2)
+    assert cb["unit"] == "GB/s" and cb["kind"] == "port" and cb["cores"] == 1
+    assert cb["value"] > 0 and cb["complex128_1_thread_gbps"] > 0
+    assert "on 1 host thread" in cb["sample"]
+    if "scipy_all_cores_gbps" in cb:
+        assert cb["scipy_all_cores_gbps"] > 0 and cb["scipy_threads"] >= 1
