@@ -36,7 +36,8 @@ def test_cpu_input_is_rejected_by_the_dispatcher():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [1, 255, 256, 257, 1 << 20])
+@pytest.mark.parametrize("n", [1, 255, 256, 257, 2047, 2048, 2049, 4096 * 3 + 2, 1 << 20,
+                               (1 << 20) + 1])
 def test_scale_matches_torch(n):
     g = torch.Generator(device="cuda").manual_seed(n)
     x = torch.randn(n, dtype=torch.complex64, device="cuda", generator=g)
