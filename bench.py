@@ -250,6 +250,7 @@ def main(argv=None) -> int:
     extra["c1_pct_of_copy"] = round(100 * value / copy_gbps, 1)
     if not args.no_extra:
         extra.update(secondary_rows(args.impl, dev))
+        extra.update(capi_rows(lib, impl, dev, stream))
         extra.update(navier_stokes_rows(args.impl, dev))
         extra.update(radio_rows(args.impl, dev))
 
@@ -354,6 +355,85 @@ def secondary_rows(impl: str, dev) -> dict:
     # rocFFT (through torch.fft) on the C1 shape, forward.
     xc = [torch.randn(BATCH, N, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
     out["c1_rocfft_c2c_1024_fwd_ms"] = round(timed(torch.fft.fft, xc), 5)
+    return out
+
+
+def capi_rows(lib, impl: int, dev, stream) -> dict:
+    """C3 and C4 again through the C ABI alone, as C1 is measured: outputs and workspaces
+    allocated once, launches on `stream` between HIP events, inputs rotating over three sets.
+    The `extra` rows above go through the PyTorch operators, whose per-call Python, dispatcher
+    and allocation work shows up when a kernel takes some 30 us."""
+    import statistics
+
+    import torch
+
+    from spectral.benchmark import fft2_modes_work, fft2_real_work
+
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    g = torch.Generator(device=dev).manual_seed(1)
+    out = {}
+    vp = ctypes.c_void_p
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(lib.spx_last_error().decode())
+
+    def workspace(query, *args):
+        count = ctypes.c_size_t(0)
+        check(query(*args, ctypes.byref(count)))
+        return torch.empty(max(1, count.value), dtype=torch.complex64, device=dev)
+
+    def time_calls(call):
+        for i in range(3):
+            call(i % 3)
+        runs = []
+        for _ in range(5):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for i in range(20):
+                call(i % 3)
+            b.record(stream)
+            b.synchronize()
+            runs.append(a.elapsed_time(b) / 20)
+        return statistics.median(runs)
+
+    def record(name, ms, nbytes):
+        out[f"{name}_capi_ms"] = round(ms, 5)
+        out[f"{name}_capi_gbps"] = round(nbytes / (ms * 1e6), 1)
+
+    strided = 1  # SPX_COLUMNS_STRIDED
+    for n, arrays in ((128, 1024), (512, 64)):
+        xs = [torch.randn(arrays, n, n, device=dev, generator=g) for _ in range(3)]
+        ys = [torch.empty(arrays, n, n // 2 + 1, dtype=torch.complex64, device=dev)
+              for _ in range(3)]
+        zs = [torch.empty(arrays, n, n, device=dev) for _ in range(3)]
+        w_f = workspace(lib.spx_fft2_r2c_workspace, impl, strided, n, n, arrays)
+        w_i = workspace(lib.spx_fft2_c2r_workspace, impl, strided, n, n, arrays)
+        torch.cuda.synchronize()
+        work = fft2_real_work(n, n, arrays)[1]
+        record(f"c3_rfft2_{n}", time_calls(lambda i: check(lib.spx_fft2_r2c(
+            impl, strided, vp(xs[i].data_ptr()), vp(ys[i].data_ptr()), n, n, arrays,
+            vp(w_f.data_ptr()), sptr))), work)
+        record(f"c3_irfft2_{n}", time_calls(lambda i: check(lib.spx_fft2_c2r(
+            impl, strided, vp(ys[i].data_ptr()), vp(zs[i].data_ptr()), n, n, arrays,
+            vp(w_i.data_ptr()), sptr))), work)
+        del xs, ys, zs, w_f, w_i
+    # C4: [64, 32, 128, 128] <-> modes [64, 32, 32, 16], m1 = m2 = 16.
+    arrays = 2048
+    xs = [torch.randn(arrays, 128, 128, device=dev, generator=g) for _ in range(3)]
+    ms = [torch.empty(arrays, 32, 16, dtype=torch.complex64, device=dev) for _ in range(3)]
+    zs = [torch.empty(arrays, 128, 128, device=dev) for _ in range(3)]
+    w_f = workspace(lib.spx_rfft2_modes_workspace, impl, 128, 128, 16, 16, arrays)
+    w_i = workspace(lib.spx_irfft2_modes_workspace, impl, 128, 128, 16, 16, arrays)
+    torch.cuda.synchronize()
+    work = fft2_modes_work(128, 128, 16, 16, arrays)[1]
+    record("c4_rfft2_modes_128_m16", time_calls(lambda i: check(lib.spx_rfft2_modes(
+        impl, vp(xs[i].data_ptr()), vp(ms[i].data_ptr()), 128, 128, 16, 16, arrays,
+        vp(w_f.data_ptr()), sptr))), work)
+    record("c4_irfft2_modes_128_m16", time_calls(lambda i: check(lib.spx_irfft2_modes(
+        impl, vp(ms[i].data_ptr()), vp(zs[i].data_ptr()), 128, 128, 16, 16, arrays,
+        vp(w_i.data_ptr()), sptr))), work)
     return out
 
 
