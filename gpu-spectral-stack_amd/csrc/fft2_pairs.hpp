@@ -48,9 +48,15 @@ struct PairRows {
 // Forward pass 2: z (arrays x n1 x M, column-transformed packed rows) -> y (arrays x n1 x (M+1)).
 struct PairR2cIo {
     static constexpr bool kGroupIsBlock = true;
+    static constexpr bool kFinal = true;
     const cf32* z;
     cf32* y;
     PairRows rows;
+
+    // Rows of 16 lanes or more rebuild and store their bins from registers (final); shorter
+    // rows go through the staged store.
+    template <class P>
+    static constexpr bool direct_combine() { return P::L >= 16; }
 
     template <class P>
     static constexpr bool direct_in() { return P::L >= 16; }
@@ -83,10 +89,58 @@ struct PairR2cIo {
         });
     }
 
+    // The last stage leaves Z[k] of this row in slot e (k = lane + off); with both rows of the
+    // pair in LDS, the lane reads the partner's Z[-k] and forms X[k1, k] = FA + W^k FB (W =
+    // exp(-pi i / N); FA, FB as in the staged store below) for its own k, one twiddle per lane,
+    // and stores it: each store is a run of L values. X[k1, N] = FA - FB at k = 0.
+    template <class P, bool WaveLocal>
+    __device__ __forceinline__ void final(cf32* s, cf32 (&v)[P::E], int lane, long long t,
+                                          long long batch) const
+    {
+        lds_sync<WaveLocal>();
+        final_write<P>(s, v, lane);
+        lds_sync<WaveLocal>();
+        if constexpr (direct_combine<P>()) {
+            constexpr int N = P::N;
+            constexpr int RL = P::template radix<P::kStages - 1>();
+            // Pairs are transforms (2 p, 2 p + 1) of one workgroup (an even number per group).
+            const cf32* const partner = (t & 1) != 0 ? s - P::kStride : s + P::kStride;
+            long long array;
+            bool dup;
+            const int r = rows.row(t, array, dup);
+            const bool live = t < batch && !dup;
+            cf32* const dst = y + (array * rows.n1 + r) * (N + 1);
+            const cf32 base = twiddle_of<2 * N, false>(lane);
+            cf32 xn{0.0f, 0.0f};
+            static_for<0, P::E>([&](auto ei) {
+                constexpr int e = decltype(ei)::value;
+                constexpr int off = (e / RL) * P::L + (e % RL) * (P::N / RL);
+                const int k = lane + off;
+                const cf32 fa = v[e];
+                const cf32 fb = partner[pad((N - k) & (N - 1))];
+                const cf32 ev{0.5f * (fa.re + fb.re), 0.5f * (fa.im - fb.im)};
+                const cf32 od{0.5f * (fa.im + fb.im), -0.5f * (fa.re - fb.re)};
+                constexpr cf32 c = const_twiddle<false>(off, 2 * N);
+                if (live) {
+                    st_stream(dst + k, cadd(ev, cmul(off == 0 ? base : cmul(base, c), od)));
+                }
+                if constexpr (off == 0) {
+                    xn = csub(ev, od);
+                }
+            });
+            if (live && lane == 0) {
+                st_stream(dst + N, xn);
+            }
+        }
+    }
+
     template <class P, class G>
     __device__ __forceinline__ void store(cf32* lds, long long first, int count,
                                           int tid) const
     {
+        if constexpr (direct_combine<P>()) {
+            return;  // stored by final
+        }
         constexpr int N = P::N;
         using S = Staged<G, N + 1>;
         S::each(count, tid, [&](int, int u, int k, bool valid) {

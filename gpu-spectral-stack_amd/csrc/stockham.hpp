@@ -662,8 +662,8 @@ template <class Io>
 struct HasStage0<Io, std::void_t<decltype(Io::kStage0)>> : std::bool_constant<Io::kStage0> {};
 
 // An I/O policy with `static constexpr bool kFinal = true` takes the last stage's outputs from
-// registers itself (final<P, WaveLocal>(s, v, lane)) and leaves in LDS what its staged store
-// reads, instead of final_write.
+// registers itself (final<P, WaveLocal>(s, v, lane, t, batch), t the lane's transform) instead of
+// final_write: it leaves in LDS what its staged store reads, or stores them itself.
 template <class Io, class = void>
 struct HasFinal : std::false_type {};
 template <class Io>
@@ -738,7 +738,7 @@ __global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch
         }
     } else {
         if constexpr (HasFinal<Io>::value) {
-            io.template final<P, kWaveGroups>(s, v, lane);
+            io.template final<P, kWaveGroups>(s, v, lane, t, batch);
         } else {
             lds_sync<kWaveGroups>();
             final_write<P>(s, v, lane);
@@ -874,7 +874,8 @@ struct R2cIo {
     // O = (Z[k] - conj Z[m-k]) / 2i (indices mod m), and X[m] = E[0] - O[0] at k = 0; then X
     // replaces Z in LDS. A lane's k are lane plus compile-time offsets: one twiddle per lane.
     template <class P, bool WaveLocal>
-    __device__ __forceinline__ void final(cf32* s, cf32 (&v)[P::E], int lane) const
+    __device__ __forceinline__ void final(cf32* s, cf32 (&v)[P::E], int lane, long long,
+                                          long long) const
     {
         lds_sync<WaveLocal>();
         final_write<P>(s, v, lane);
