@@ -43,6 +43,22 @@ struct PairRows {
         dup = slot && (k1 == 0 || 2 * k1 == n1);
         return slot ? (n1 - k1) & (n1 - 1) : k1;
     }
+
+    // The same for t = first + du, 0 <= du, given first's pair split once as (array0, k10) with
+    // `first` even: no division per transform.
+    __device__ __forceinline__ int row_after(long long array0, int k10, int du, long long& array,
+                                             bool& dup) const
+    {
+        int k1 = k10 + (du >> 1);
+        array = array0;
+        while (k1 >= pairs) {
+            k1 -= pairs;
+            ++array;
+        }
+        const bool slot = (du & 1) != 0;
+        dup = slot && (k1 == 0 || 2 * k1 == n1);
+        return slot ? (n1 - k1) & (n1 - 1) : k1;
+    }
 };
 
 // Forward pass 2: z (arrays x n1 x M, column-transformed packed rows) -> y (arrays x n1 x (M+1)).
@@ -78,9 +94,19 @@ struct PairR2cIo {
     __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
     {
         using S = Staged<G, P::N>;
+        // The group's first transform is even (groups hold an even number): split its pair once.
+        const long long array0 = (first >> 1) / rows.pairs;
+        const int k10 = static_cast<int>((first >> 1) - array0 * rows.pairs);
         cf32 val[S::kSteps];
         S::each(count, tid, [&](int k, int u, int i, bool valid) {
-            val[k] = valid ? in<P>(first + u, i) : czero();
+            cf32 v = czero();
+            if (valid) {
+                long long array;
+                bool dup;
+                const int r = rows.row_after(array0, k10, u, array, dup);
+                v = z[(array * rows.n1 + r) * P::N + i];
+            }
+            val[k] = v;
         });
         S::each(count, tid, [&](int k, int u, int i, bool valid) {
             if (valid) {
@@ -143,10 +169,12 @@ struct PairR2cIo {
         }
         constexpr int N = P::N;
         using S = Staged<G, N + 1>;
+        const long long array0 = (first >> 1) / rows.pairs;
+        const int k10 = static_cast<int>((first >> 1) - array0 * rows.pairs);
         S::each(count, tid, [&](int, int u, int k, bool valid) {
             long long array;
             bool dup;
-            const int r = rows.row(first + u, array, dup);
+            const int r = rows.row_after(array0, k10, u, array, dup);
             if (!valid || dup) {
                 return;
             }
@@ -196,13 +224,16 @@ struct PairC2rIo {
         constexpr int N = P::N;
         static_assert(pad(N) < P::kStride, "a row of N + 1 values fits its LDS stride");
         using S = Staged<G, N + 1>;
+        // The group's first transform is even (groups hold an even number): split its pair once.
+        const long long array0 = (first >> 1) / rows.pairs;
+        const int k10 = static_cast<int>((first >> 1) - array0 * rows.pairs);
         cf32 val[S::kSteps];
         S::each(count, tid, [&](int k, int u, int i, bool valid) {
             cf32 v = czero();
             if (valid) {
                 long long array;
                 bool dup;
-                const int r = rows.row(first + u, array, dup);
+                const int r = rows.row_after(array0, k10, u, array, dup);
                 v = x[(array * rows.n1 + r) * (N + 1) + i];
             }
             val[k] = v;
@@ -249,9 +280,15 @@ struct PairC2rIo {
                                           int tid) const
     {
         using S = Staged<G, P::N>;
+        const long long array0 = (first >> 1) / rows.pairs;
+        const int k10 = static_cast<int>((first >> 1) - array0 * rows.pairs);
         S::each(count, tid, [&](int, int u, int i, bool valid) {
-            if (valid) {
-                out<P>(first + u, i, lds[u * P::kStride + pad(i)]);
+            long long array;
+            bool dup;
+            const int r = rows.row_after(array0, k10, u, array, dup);
+            if (valid && !dup) {
+                st_stream(z + (array * rows.n1 + r) * P::N + i,
+                          cscale(lds[u * P::kStride + pad(i)], scale));
             }
         });
     }

@@ -254,3 +254,50 @@ def test_direct_radio_and_navier_stokes_calls(lib, rng):
                                                      2.5e-3, 64)
     torch.cuda.synchronize()
     assert torch.equal(f0, ref_f0) and torch.equal(pred, ref_pred)
+
+
+def _fft_columns(x: np.ndarray, inverse: bool) -> np.ndarray:
+    from oracle import reference as ref
+
+    cols_last = np.swapaxes(x, -1, -2)
+    return np.swapaxes(ref.ifft(cols_last) if inverse else ref.fft(cols_last), -1, -2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(("n", "slabs"), [(256, 1040), (512, 300)])
+def test_direct_columns_over_many_tiles(lib, rng, n, slabs):
+    # 17 columns per slab: more tiles of 16 columns than the device holds workgroups at once, so
+    # each workgroup of the persistent column kernel walks several, and the last tile is partial.
+    # Out of place and in place, forward and inverse, and both pruned sides.
+    from oracle.tolerance import assert_transform_close, random_complex
+
+    cols, m1 = 17, 8
+    x = random_complex(rng, (slabs, n, cols))
+    xd = torch.from_numpy(x).cuda()
+    for inverse in (0, 1):
+        yd = torch.empty_like(xd)
+        assert lib.spx_columns(3, _ptr(xd), _ptr(yd), n, cols, slabs, inverse, None) == SPX_OK
+        inplace = xd.clone()
+        assert lib.spx_columns(3, _ptr(inplace), _ptr(inplace), n, cols, slabs, inverse,
+                               None) == SPX_OK
+        torch.cuda.synchronize()
+        expected = _fft_columns(x, bool(inverse))
+        assert_transform_close(yd, expected, n, axes=(-2,))
+        assert torch.equal(inplace, yd)
+
+    # Forward keeping rows 0 .. m1-1 and n-m1 .. n-1; inverse from those rows alone.
+    kept = torch.empty(slabs, 2 * m1, cols, dtype=torch.complex64, device="cuda")
+    assert lib.spx_pruned_columns(3, _ptr(xd), _ptr(kept), n, cols, slabs, 0, m1, 0,
+                                  None) == SPX_OK
+    full = _fft_columns(x, False)
+    rows = np.r_[0:m1, n - m1:n]
+    modes = random_complex(rng, (slabs, 2 * m1, cols))
+    md = torch.from_numpy(modes).cuda()
+    back = torch.empty_like(xd)
+    assert lib.spx_pruned_columns(3, _ptr(md), _ptr(back), n, cols, slabs, m1, 0, 1,
+                                  None) == SPX_OK
+    torch.cuda.synchronize()
+    assert_transform_close(kept, full[:, rows, :], n, axes=(-2,))
+    padded = np.zeros((slabs, n, cols), dtype=np.complex64)
+    padded[:, rows, :] = modes
+    assert_transform_close(back, _fft_columns(padded, True), n, axes=(-2,))
