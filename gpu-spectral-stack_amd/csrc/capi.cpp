@@ -358,4 +358,12 @@ int spx_rf_fir(int impl, const void* x, const void* h, void* y, long long n, int
     });
 }
 
+int spx_rf_fir_spectrum(int impl, const void* taps, int complex_taps, void* h, int count,
+                        int nfft, hipStream_t stream)
+{
+    return guarded([&] {
+        rf_of(impl_at(impl)).filter(taps, complex_taps != 0, cm(h), count, nfft, stream);
+    });
+}
+
 }  // extern "C"

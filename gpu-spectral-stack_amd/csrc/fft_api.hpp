@@ -70,6 +70,9 @@ struct RfFns {
     // y (rows, n) = x filtered by the taps whose nfft-point spectrum is h (taps <= nfft).
     void (*fir)(const cf32* x, const cf32* h, cf32* y, long long n, int taps, int nfft,
                 long long rows, hipStream_t stream);
+    // h (nfft) = FFT of the taps (float32, or complex64 when complex_taps) zero-padded to nfft.
+    void (*filter)(const void* taps, bool complex_taps, cf32* h, int count, int nfft,
+                   hipStream_t stream);
     int max_nfft;
 };
 

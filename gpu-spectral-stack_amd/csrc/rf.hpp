@@ -88,6 +88,60 @@ struct FramesIo {
     }
 };
 
+// The FIR's filter spectrum h: one transform of N points whose input i is tap i (real float32 or
+// complex64), zero from i = taps on. The reference builds it with torch ops around its FFT
+// (python/spectral/rf.py:145-147: zeros, a copy of the converted taps, fft); this is one launch.
+struct TapsIo {
+    static constexpr bool kGroupIsBlock = false;
+    const void* taps;
+    bool complex_taps;
+    int count;
+    cf32* h;
+
+    template <class P>
+    static constexpr bool direct_in() { return P::L >= 16; }
+    template <class P>
+    static constexpr bool direct_out() { return P::L >= 16; }
+
+    template <class P>
+    __device__ __forceinline__ cf32 in(long long, int i) const
+    {
+        if (i >= count) {
+            return czero();
+        }
+        return complex_taps ? static_cast<const cf32*>(taps)[i]
+                            : cf32{static_cast<const float*>(taps)[i], 0.0f};
+    }
+
+    template <class P>
+    __device__ __forceinline__ void out(long long, int i, cf32 v) const
+    {
+        h[i] = v;
+    }
+
+    template <class P, class G>
+    __device__ __forceinline__ void load(cf32* lds, long long first, int count_, int tid) const
+    {
+        using S = Staged<G, P::N>;
+        S::each(count_, tid, [&](int, int u, int i, bool valid) {
+            if (valid) {
+                lds[u * P::kStride + pad(i)] = in<P>(first + u, i);
+            }
+        });
+    }
+
+    template <class P, class G>
+    __device__ __forceinline__ void store(cf32* lds, long long, int count_, int tid) const
+    {
+        using S = Staged<G, P::N>;
+        S::each(count_, tid, [&](int, int u, int i, bool valid) {
+            if (valid) {
+                h[i] = lds[u * P::kStride + pad(i)];
+            }
+        });
+    }
+};
+
 // Overlap-save blocks: transform t = row * blocks + b.
 template <class P, bool Table>
 __global__ void __launch_bounds__(P::kThreads)

@@ -448,6 +448,27 @@ at::Tensor rf_fir_op(const at::Tensor& x, const at::Tensor& h, int64_t taps, int
     return y;
 }
 
+// The FIR's filter spectrum from its taps (float32 or complex64, on the device), one launch.
+at::Tensor rf_fir_spectrum_op(const at::Tensor& taps, int64_t nfft, c10::string_view impl_name)
+{
+    TORCH_CHECK_VALUE(taps.is_cuda() && (taps.scalar_type() == at::kFloat
+                                         || taps.scalar_type() == at::kComplexFloat),
+                      "taps must be a float32 or complex64 CUDA tensor, got ", taps.scalar_type(),
+                      " on ", taps.device());
+    TORCH_CHECK_VALUE(taps.dim() == 1 && taps.numel() >= 1, "taps must be a non-empty 1D tensor");
+    const Impl impl = find_impl(impl_name);
+    TORCH_CHECK_VALUE(spx_rf_max_nfft(impl.index) > 0, impl.info.name,
+                      " has no fused radio kernels");
+    at::Tensor h = at::empty({nfft}, taps.options().dtype(at::kComplexFloat));
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(taps.device());
+    const at::Tensor tc = taps.contiguous();
+    check_status(spx_rf_fir_spectrum(impl.index, tc.data_ptr(),
+                                     taps.scalar_type() == at::kComplexFloat ? 1 : 0, mptr(h),
+                                     static_cast<int>(taps.numel()), static_cast<int>(nfft),
+                                     current_stream()));
+    return h;
+}
+
 // --- the Navier-Stokes caller: one fused IMEX stage per field (no reference operator; the
 // reference's GpuSolver composes its transforms with torch elementwise ops instead) ----------
 
@@ -575,6 +596,7 @@ TORCH_LIBRARY(spectral, m)
     // The radio callers' fused kernels (no reference operator).
     m.def("rf_spectrum(Tensor x, Tensor? window, int nfft, str impl) -> Tensor");
     m.def("rf_fir(Tensor x, Tensor h, int taps, int nfft, str impl) -> Tensor");
+    m.def("rf_fir_spectrum(Tensor taps, int nfft, str impl) -> Tensor");
     // The Navier-Stokes caller's fused stages (no reference operator).
     m.def("ns_predict(Tensor w_hat, Tensor forcing_hat, Tensor nu, float drag, float dt, int n)"
           " -> (Tensor, Tensor)");
@@ -596,6 +618,7 @@ TORCH_LIBRARY_IMPL(spectral, CUDA, m)
     m.impl("irfft2_modes", &irfft2_modes_op);
     m.impl("rf_spectrum", &rf_spectrum_op);
     m.impl("rf_fir", &rf_fir_op);
+    m.impl("rf_fir_spectrum", &rf_fir_spectrum_op);
     m.impl("ns_predict", &ns_predict_op);
     m.impl("ns_correct", &ns_correct_op);
 }

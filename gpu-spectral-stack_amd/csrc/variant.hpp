@@ -1067,7 +1067,21 @@ struct RfDriver {
         });
     }
 
-    static RfFns fns() { return {&spectrum, &fir, kSinglePassMaxN}; }
+    static void filter(const void* taps, bool complex_taps, cf32* h, int count, int nfft,
+                       hipStream_t stream)
+    {
+        check(0, nfft, 0, "fir");
+        if (count < 1 || count > nfft) {
+            throw InvalidArgument("fir: nfft must be a power of two of at least len(taps) = "
+                                  + str(count) + ", got " + str(nfft));
+        }
+        const dev::TapsIo io{taps, complex_taps, count, h};
+        by_size(nfft, [&](auto size) {
+            dev::launch<PlanOf<decltype(size)::value>, false, Table>(io, 1, stream);
+        });
+    }
+
+    static RfFns fns() { return {&spectrum, &fir, &filter, kSinglePassMaxN}; }
 };
 
 }  // namespace spx

@@ -161,11 +161,17 @@ def fir(
     if nfft < m or nfft & (nfft - 1):
         raise ValueError(f"nfft must be a power of two of at least len(taps) = {m}, got {nfft}")
 
+    if _fused(fft_impl, nfft):
+        # The filter spectrum in one launch from the taps as they are (float32 or complex64).
+        t = taps.to(device=x.device)
+        if t.dtype not in (torch.float32, torch.complex64):
+            t = t.to(torch.complex64 if t.is_complex() else torch.float32)
+        spectrum_h = torch.ops.spectral.rf_fir_spectrum.default(t, nfft, fft_impl)
+        return torch.ops.spectral.rf_fir.default(x, spectrum_h, m, nfft, fft_impl)
+
     h = torch.zeros(nfft, dtype=torch.complex64, device=x.device)
     h[:m] = taps.to(device=x.device, dtype=torch.complex64)
     spectrum_h = fft(h, fft_impl=fft_impl)
-    if _fused(fft_impl, nfft):
-        return torch.ops.spectral.rf_fir.default(x, spectrum_h, m, nfft, fft_impl)
 
     step = nfft - m + 1  # new outputs per block
     n = x.shape[-1]

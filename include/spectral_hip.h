@@ -158,12 +158,17 @@ int spx_ns_stage(const void* state, const void* w0, const void* f0, void* out_f,
  *                    (nfft floats; NULL for the rectangular window).
  *   spx_rf_fir       y (rows, n): x filtered by a causal FIR of `taps` taps (1 <= taps <= nfft)
  *                    with zero initial state, by overlap-save in blocks of nfft; h is the nfft-point
- *                    forward FFT of the taps zero-padded to nfft (complex64). */
+ *                    forward FFT of the taps zero-padded to nfft (complex64).
+ *   spx_rf_fir_spectrum  that h from `count` taps (float32, or complex64 when complex_taps != 0),
+ *                    1 <= count <= nfft, in one launch; it replaces rf.py:145-147 (zeros, a copy
+ *                    of the converted taps, fft). */
 int spx_rf_max_nfft(int impl);
 int spx_rf_spectrum(int impl, const void* x, const float* window, void* y, long long n, int nfft,
                     long long rows, hipStream_t stream);
 int spx_rf_fir(int impl, const void* x, const void* h, void* y, long long n, int taps, int nfft,
                long long rows, hipStream_t stream);
+int spx_rf_fir_spectrum(int impl, const void* taps, int complex_taps, void* h, int count,
+                        int nfft, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -247,6 +247,46 @@ def test_fir_of_an_empty_signal_is_empty(fft_impl):
 
 
 @gpu
+@pytest.mark.parametrize("fft_impl", OURS)
+@pytest.mark.parametrize("nfft", [2, 4, 16, 64, 256, 4096, 16384])
+@pytest.mark.parametrize("complex_taps", [False, True])
+def test_filter_spectrum_is_the_fft_of_the_padded_taps(rng, fft_impl, nfft, complex_taps):
+    # rf_fir_spectrum reads the taps as they are (float32 or complex64) and zero-pads them in its
+    # load: the nfft-point FFT of the taps followed by zeros (rf.py:145-147 of the reference).
+    from oracle.tolerance import fft_tolerance
+
+    for m in sorted({1, nfft // 2 + 1, nfft}):
+        taps = random_complex(rng, m) if complex_taps else random_real(rng, m)
+        h = torch.ops.spectral.rf_fir_spectrum(cuda(taps), nfft, fft_impl)
+        padded = np.zeros(nfft, dtype=np.complex128)
+        padded[:m] = taps
+        assert h.shape == (nfft,) and h.dtype == torch.complex64
+        assert relative_error(h.cpu().numpy(), np.fft.fft(padded)) < fft_tolerance(nfft)
+
+
+@gpu
+@pytest.mark.parametrize("fft_impl", OURS)
+def test_fir_converts_other_tap_types(rng, fft_impl):
+    x = random_complex(rng, 3000)
+    taps = random_real(rng, 63).astype(np.float64)
+    expected = scipy.signal.lfilter(taps, 1.0, x.astype(np.complex128))
+    for t in (cuda(taps), cuda(taps).to(torch.complex128), torch.from_numpy(taps)):
+        y = rf.fir(cuda(x), t, fft_impl=fft_impl)
+        assert relative_error(y.cpu().numpy(), expected) < 2e-5
+
+
+@gpu
+def test_filter_spectrum_rejects_bad_arguments():
+    taps = torch.ones(65, device="cuda")
+    with pytest.raises(ValueError, match="at least len\\(taps\\) = 65"):
+        torch.ops.spectral.rf_fir_spectrum(taps, 64, "stockham_r8")
+    with pytest.raises(ValueError, match="float32 or complex64"):
+        torch.ops.spectral.rf_fir_spectrum(taps.double(), 64, "stockham_r8")
+    with pytest.raises(ValueError, match="no fused radio kernels"):
+        torch.ops.spectral.rf_fir_spectrum(taps, 128, "naive")
+
+
+@gpu
 def test_fir_rejects_a_block_shorter_than_the_filter():
     x = torch.zeros(100, dtype=torch.complex64, device="cuda")
     with pytest.raises(ValueError, match="at least len\\(taps\\) = 65"):
