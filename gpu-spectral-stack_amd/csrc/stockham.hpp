@@ -838,10 +838,19 @@ struct R2cIo {
     cf32* y;
     int keep;
 
-    // The combine done by the transform's own lanes from their registers (final) for m = 8 ..
-    // 64, a separate pass over the pairs otherwise.
+    // Rows of 64 lanes or more (m >= 512 at radix 8) store their bins X[k] straight from
+    // registers, each store a run of L values, with no staged store behind. Rows of m + 1 values
+    // start at 8-byte offsets: shorter runs, from 16 or 32 lanes, measured 7-23 points slower
+    // than the staged store's contiguous run per workgroup.
     template <class P>
-    static constexpr bool direct_combine() { return P::N >= 8 && P::N <= 64; }
+    static constexpr bool direct_store() { return P::L >= 64; }
+    // The combine done by the transform's own lanes from their registers (final) for m = 8 ..
+    // 64 and with the direct store, a separate pass over the pairs otherwise.
+    template <class P>
+    static constexpr bool direct_combine()
+    {
+        return (P::N >= 8 && P::N <= 64) || direct_store<P>();
+    }
 
     template <class P>
     static constexpr bool direct_in() { return P::L >= 16; }
@@ -874,8 +883,8 @@ struct R2cIo {
     // O = (Z[k] - conj Z[m-k]) / 2i (indices mod m), and X[m] = E[0] - O[0] at k = 0; then X
     // replaces Z in LDS. A lane's k are lane plus compile-time offsets: one twiddle per lane.
     template <class P, bool WaveLocal>
-    __device__ __forceinline__ void final(cf32* s, cf32 (&v)[P::E], int lane, long long,
-                                          long long) const
+    __device__ __forceinline__ void final(cf32* s, cf32 (&v)[P::E], int lane, long long t,
+                                          long long batch) const
     {
         lds_sync<WaveLocal>();
         final_write<P>(s, v, lane);
@@ -899,12 +908,28 @@ struct R2cIo {
                     xm = csub(ev, od);  // X[m], kept by the lane with k = 0
                 }
             });
-            lds_sync<WaveLocal>();  // every partner read is done before X replaces Z
-            final_write<P>(s, v, lane);
-            if (lane == 0) {
-                s[pad(m)] = xm;
+            if constexpr (direct_store<P>()) {
+                if (t < batch) {
+                    cf32* const dst = y + t * keep;
+                    static_for<0, P::E>([&](auto ei) {
+                        constexpr int e = decltype(ei)::value;
+                        constexpr int off = (e / RL) * P::L + (e % RL) * (P::N / RL);
+                        if (lane + off < keep) {
+                            st_stream(dst + lane + off, v[e]);
+                        }
+                    });
+                    if (lane == 0 && m < keep) {
+                        st_stream(dst + m, xm);
+                    }
+                }
+            } else {
+                lds_sync<WaveLocal>();  // every partner read is done before X replaces Z
+                final_write<P>(s, v, lane);
+                if (lane == 0) {
+                    s[pad(m)] = xm;
+                }
+                lds_sync<WaveLocal>();
             }
-            lds_sync<WaveLocal>();
         }
     }
 
@@ -912,6 +937,9 @@ struct R2cIo {
     __device__ __forceinline__ void store(cf32* lds, long long first, int count, int tid) const
     {
         constexpr int m = P::N;
+        if constexpr (direct_store<P>()) {
+            return;  // stored by final
+        }
         if constexpr (!direct_combine<P>()) {
             // 1. Combine in place: pair k reads Z[k] and Z[m-k] and writes X[k] and X[m-k] to the
             //    same two slots (k = 0 reads slot 0 and writes X[0] there and X[m] into slot m),
