@@ -168,8 +168,7 @@ void fft2_r2c(const FftImpl& impl, Columns columns, const float* x, cf32* y, int
         return;
     }
     if (column_first(impl, columns, n1, n2)) {
-        impl.columns(reinterpret_cast<const cf32*>(x), work, n1, n2 / 2, batch,
-                     Direction::Forward, stream);
+        impl.fused->r2c_columns(reinterpret_cast<const cf32*>(x), work, n1, n2 / 2, batch, stream);
         impl.fused->r2c_rows(work, y, n1, n2 / 2, batch, stream);
         return;
     }

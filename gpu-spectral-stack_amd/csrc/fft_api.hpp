@@ -50,6 +50,9 @@ struct Fused2dFns {
                 hipStream_t stream);
     void (*c2r)(const cf32* x, float* y, int n1, int n2, int m1, int w, int batch,
                 hipStream_t stream);
+    // The column-first forward's column pass: x (batch x n1 x m packed real rows) -> z, the
+    // workspace the row-pair pass reads (kept in the caches where it can be).
+    void (*r2c_columns)(const cf32* x, cf32* z, int n1, int m, int batch, hipStream_t stream);
     // Row-pair passes of the column-first 2D real transforms (fft2_pairs.hpp), m = n2 / 2 from
     // 16 to 4096: z (batch x n1 x m, column-transformed packed rows) -> y (batch x n1 x (m + 1)),
     // and x (batch x n1 x (m + 1)) -> z (prepared, row-inverted, scaled by 1 / m).

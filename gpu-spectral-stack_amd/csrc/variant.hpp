@@ -475,7 +475,7 @@ struct Stockham {
         const bool inverse = direction == Direction::Inverse;
         const std::size_t total = static_cast<std::size_t>(n) * static_cast<std::size_t>(batch);
         StreamWorkspace work(total, stream);
-        columns_impl(x, work.get(), n1, n2, batch, direction, stream, 0, 0);
+        columns_impl(x, work.get(), n1, n2, batch, direction, stream, 0, 0, false);
         const dev::TwiddleRowsTransposedIo rows{
             dev::TwiddleRowsIo{work.get(), y, inverse ? 1.0f / static_cast<float>(n2) : 1.0f,
                                inverse ? 1.0f : -1.0f, n1, 2.0f / static_cast<float>(n)},
@@ -545,7 +545,7 @@ struct Stockham {
         const bool inverse = direction == Direction::Inverse;
         StreamWorkspace work(total, stream);
         // 1. n1-point transforms down the n2 columns of each n1 x n2 matrix (x -> y).
-        columns_impl(x, y, n1, n2, batch, direction, stream, 0, 0);
+        columns_impl(x, y, n1, n2, batch, direction, stream, 0, 0, false);
         // 2 + 3. Twiddle, then n2-point rows (y -> work).
         const dev::TwiddleRowsIo rows{y,
                                       work.get(),
@@ -615,8 +615,11 @@ struct Stockham {
         }
     }
 
+    // stream_out: y is a final output (nontemporal stores); false for an intermediate that the
+    // next pass reads.
     static void columns_impl(const cf32* x, cf32* y, int n, int cols, int slabs,
-                             Direction direction, hipStream_t stream, int m1_in, int m1_out)
+                             Direction direction, hipStream_t stream, int m1_in, int m1_out,
+                             bool stream_out = true)
     {
         check_size(n, "stockham columns");
         if (cols < 1 || slabs < 1 || static_cast<long long>(cols) * slabs > INT_MAX) {
@@ -642,7 +645,7 @@ struct Stockham {
         }
         const bool inverse = direction == Direction::Inverse;
         const float scale = inverse ? 1.0f / static_cast<float>(n) : 1.0f;
-        const dev::StridedIo io{x, y, cols, scale, m1_in, m1_out};
+        const dev::StridedIo io{x, y, cols, scale, m1_in, m1_out, stream_out};
         if (inverse) {
             dev::dispatch_strided_columns<R, true, Table>(n, io, batch, stream);
         } else {
@@ -952,6 +955,13 @@ struct Fused2dDriver {
         }
     }
 
+    // The forward's column pass, into the workspace that r2c_rows reads next (plain stores).
+    static void r2c_columns(const cf32* x, cf32* z, int n1, int m, int batch, hipStream_t stream)
+    {
+        Stockham<R, Table>::columns_impl(x, z, n1, m, batch, Direction::Forward, stream, 0, 0,
+                                         false);
+    }
+
     static void r2c_rows(const cf32* z, cf32* y, int n1, int m, int batch, hipStream_t stream)
     {
         const dev::PairRows rows{n1, n1 / 2 + 1};
@@ -967,7 +977,7 @@ struct Fused2dDriver {
 
     static Fused2dFns fns()
     {
-        return {&supports, &r2c, &c2r, &r2c_rows, &c2r_rows, &c2c_supports, &c2c};
+        return {&supports, &r2c, &c2r, &r2c_columns, &r2c_rows, &c2r_rows, &c2c_supports, &c2c};
     }
 
     static void c2r(const cf32* x, float* y, int n1, int n2, int m1, int w, int batch,
