@@ -1136,10 +1136,10 @@ struct StridedIo {
 
     // The global half of the load: lane tid takes column j = tid mod T of the tile starting at
     // transform `first`, rows tid / T + k kThreads / T, into registers (zero for the rows a pruned
-    // input does not hold). Lanes of columns past `count` take nothing.
+    // input does not hold). Lanes of columns past `count` take nothing. nt: nontemporal loads.
     template <class P, bool Full>
     __device__ __forceinline__ void fetch(cf32 (&val)[steps<P>()], long long first, int count,
-                                          int tid) const
+                                          int tid, bool nt = false) const
     {
         constexpr int kRowsPerStep = P::kThreads / P::T;
         const int j = tid % P::T;
@@ -1158,7 +1158,8 @@ struct StridedIo {
             if (m1_in > 0) {
                 row = i < m1_in ? i : (i >= P::N - m1_in ? i - (P::N - rows) : -1);
             }
-            val[k] = row >= 0 ? base[static_cast<long long>(row) * cols] : czero();
+            const cf32* const src = base + static_cast<long long>(row) * cols;
+            val[k] = row < 0 ? czero() : (nt ? ld_stream(src) : *src);
         }
     }
 
@@ -1241,10 +1242,14 @@ __global__ void __launch_bounds__(P::kThreads)
         const long long left = batch - tile * P::T;
         return left >= P::T ? P::T : static_cast<int>(left);
     };
+    // The last pass of a transform (final output) also loads nontemporally: 1 point of the peak
+    // faster for the inverse 2D and fft2_c2c column passes at 256 and 512 points, where the
+    // forward's first pass measured 1-2 points slower with it.
+    const bool nt = io.stream_out;
     cf32 val[StridedIo::steps<P>()];
     long long tile = blockIdx.x;
     if (tile < tiles) {
-        io.template fetch<P, false>(val, tile * P::T, count_of(tile), tid);
+        io.template fetch<P, false>(val, tile * P::T, count_of(tile), tid, nt);
     }
     for (; tile < tiles; tile += gridDim.x) {
         const int count = count_of(tile);
@@ -1252,7 +1257,7 @@ __global__ void __launch_bounds__(P::kThreads)
         lds_sync<false>();
         const long long next = tile + gridDim.x;
         if (next < tiles) {
-            io.template fetch<P, false>(val, next * P::T, count_of(next), tid);
+            io.template fetch<P, false>(val, next * P::T, count_of(next), tid, nt);
         }
         // Columns past the batch run the stages on what the tile holds but store nothing.
         cf32 v[P::E];
