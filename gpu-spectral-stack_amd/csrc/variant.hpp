@@ -325,6 +325,8 @@ struct ColumnStepIo {
     bool twiddle;
     float sign;
     float two_over_n;
+    bool stream_in;   // nontemporal loads (a caller's input), else plain (the pass-A workspace)
+    bool stream_out;  // nontemporal stores (a final output), else plain (a workspace read next)
 
     template <class P>
     static constexpr bool direct_in() { return false; }
@@ -362,7 +364,7 @@ struct ColumnStepIo {
 #pragma unroll
         for (int k = 0; k < kSteps; ++k) {
             const int i = tid / P::T + k * kRowsPerStep;
-            val[k] = ld_stream(base + i * stride_in);
+            val[k] = stream_in ? ld_stream(base + i * stride_in) : base[i * stride_in];
         }
 #pragma unroll
         for (int k = 0; k < kSteps; ++k) {
@@ -391,7 +393,11 @@ struct ColumnStepIo {
                 w.im *= sign;
                 v = cmul(v, w);
             }
-            st_stream(base + i * stride_out, v);
+            if (stream_out) {
+                st_stream(base + i * stride_out, v);
+            } else {
+                base[i * stride_out] = v;
+            }
         }
     }
 };
@@ -570,7 +576,7 @@ struct Stockham {
     // the 64-point transforms over rows j1 (n/64) + j2 and twiddles them (x -> work); pass B runs
     // the (n/64)-point transforms over rows k1 (n/64) + j2 and writes row k1 + 64 k2 (work -> y).
     static void long_columns(const cf32* x, cf32* y, int n, int cols, int slabs,
-                             Direction direction, hipStream_t stream)
+                             Direction direction, hipStream_t stream, bool stream_out)
     {
         constexpr int n1c = 64;
         const int n2c = n / n1c;
@@ -590,7 +596,9 @@ struct Stockham {
                                   1.0f,
                                   true,
                                   inverse ? 1.0f : -1.0f,
-                                  2.0f / static_cast<float>(n)};
+                                  2.0f / static_cast<float>(n),
+                                  true,
+                                  false};
         const dev::ColumnStepIo b{work.get(),
                                   y,
                                   cols,
@@ -603,7 +611,9 @@ struct Stockham {
                                   inverse ? 1.0f / static_cast<float>(n) : 1.0f,
                                   false,
                                   1.0f,
-                                  0.0f};
+                                  0.0f,
+                                  false,
+                                  stream_out};
         const long long transforms_a = static_cast<long long>(slabs) * n2c * cols;
         const long long transforms_b = static_cast<long long>(slabs) * n1c * cols;
         if (inverse) {
@@ -633,7 +643,7 @@ struct Stockham {
         }
         const long long batch = static_cast<long long>(cols) * slabs;
         if (n >= 2048 && m1_in == 0 && m1_out == 0 && cols >= 32) {
-            long_columns(x, y, n, cols, slabs, direction, stream);
+            long_columns(x, y, n, cols, slabs, direction, stream, stream_out);
             return;
         }
         if (n == 1) {
