@@ -845,11 +845,12 @@ struct R2cIo {
     template <class P>
     static constexpr bool direct_store() { return P::L >= 64; }
     // The combine done by the transform's own lanes from their registers (final) for m = 8 ..
-    // 64 and with the direct store, a separate pass over the pairs otherwise.
+    // 64 and for rows of 16 lanes or more (X then goes back to LDS for the staged store, or out
+    // directly), a separate pass over the pairs otherwise.
     template <class P>
     static constexpr bool direct_combine()
     {
-        return (P::N >= 8 && P::N <= 64) || direct_store<P>();
+        return (P::N >= 8 && P::N <= 64) || P::L >= 16;
     }
 
     template <class P>
