@@ -301,3 +301,23 @@ def test_direct_columns_over_many_tiles(lib, rng, n, slabs):
     padded = np.zeros((slabs, n, cols), dtype=np.complex64)
     padded[:, rows, :] = modes
     assert_transform_close(back, _fft_columns(padded, True), n, axes=(-2,))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [256, 512, 1024, 2048, 4096, 8192])
+def test_direct_pruned_r2c_at_every_row_width(lib, rng, n):
+    # R2C rows of 16 .. 256 lanes at radix 8: the register combine with the staged store (16, 32
+    # lanes) and with the direct store (64 lanes and more), each keeping 1 .. n/2 + 1 bins; a batch
+    # of 37 rows leaves the last workgroup partly empty.
+    from oracle import reference as ref
+    from oracle.tolerance import assert_transform_close, random_real
+
+    batch, m = 37, n // 2
+    x = random_real(rng, (batch, n))
+    xd = torch.from_numpy(x).cuda()
+    full = ref.rfft(x)
+    for keep in (1, 7, m // 2, m, m + 1):
+        yd = torch.empty(batch, keep, dtype=torch.complex64, device="cuda")
+        assert lib.spx_pruned_r2c(3, _ptr(xd), _ptr(yd), n, batch, keep, None) == SPX_OK
+        torch.cuda.synchronize()
+        assert_transform_close(yd, full[:, :keep], n)
