@@ -124,6 +124,8 @@ inline int device_cus()
 }
 
 // The persistent strided column kernel over as many workgroups as fit on the device at once.
+// Workgroups per CU depend only on the kernel and the architecture (gfx950 everywhere this
+// library runs), so the first query serves every device; the CU count is per device.
 template <class P, bool Inv, bool Table>
 void launch_columns_persistent(const StridedIo& io, long long batch, hipStream_t stream)
 {
