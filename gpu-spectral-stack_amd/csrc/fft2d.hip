@@ -134,7 +134,11 @@ void fft2_c2c(const FftImpl& impl, Columns columns, const cf32* x, cf32* y, int 
         return;
     }
     if (columns == Columns::Strided) {
-        impl.c2c(x, y, n2, batch * n1, direction, stream);
+        if (impl.fused != nullptr) {
+            impl.fused->c2c_rows(x, y, n2, batch * n1, direction, stream);
+        } else {
+            impl.c2c(x, y, n2, batch * n1, direction, stream);
+        }
         impl.columns(y, y, n1, n2, batch, direction, stream);
         return;
     }

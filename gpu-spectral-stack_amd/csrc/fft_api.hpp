@@ -62,6 +62,10 @@ struct Fused2dFns {
     bool (*c2c_supports)(int n1, int n2);
     void (*c2c)(const cf32* x, cf32* y, int n1, int n2, int batch, Direction direction,
                 hipStream_t stream);
+    // The row pass of the row-then-column complex 2D (batch rows of n), into y, which the column
+    // pass then transforms in place (plain stores).
+    void (*c2c_rows)(const cf32* x, cf32* y, int n, int batch, Direction direction,
+                     hipStream_t stream);
 };
 
 // The radio callers (rf.hpp): windowed spectrum of back-to-back frames, and overlap-save FIR.

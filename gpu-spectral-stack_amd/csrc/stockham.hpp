@@ -755,8 +755,9 @@ __global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch
 // --- I/O policies ---------------------------------------------------------------------------
 
 // Contiguous complex rows. Pruned: rows of x hold keep_in values (the rest of each transform is
-// zero), rows of y keep_out values.
-template <bool Pruned>
+// zero), rows of y keep_out values. PlainOut: plain stores, for an intermediate that the next
+// pass reads (nontemporal otherwise).
+template <bool Pruned, bool PlainOut = false>
 struct C2cIo {
     static constexpr bool kGroupIsBlock = false;
     const cf32* x;
@@ -785,10 +786,10 @@ struct C2cIo {
     {
         if constexpr (Pruned) {
             if (i < keep_out) {
-                st_stream(y + t * keep_out + i, cscale(v, scale));
+                put(y + t * keep_out + i, cscale(v, scale));
             }
         } else {
-            st_stream(y + t * P::N + i, cscale(v, scale));
+            put(y + t * P::N + i, cscale(v, scale));
         }
     }
 
@@ -818,9 +819,18 @@ struct C2cIo {
         cf32* dst = y + first * row;
         S::each(count, tid, [&](int, int u, int i, bool valid) {
             if (valid && (!Pruned || i < keep_out)) {
-                st_stream(dst + u * row + i, cscale(lds[u * P::kStride + pad(i)], scale));
+                put(dst + u * row + i, cscale(lds[u * P::kStride + pad(i)], scale));
             }
         });
+    }
+
+    __device__ __forceinline__ static void put(cf32* p, cf32 v)
+    {
+        if constexpr (PlainOut) {
+            *p = v;
+        } else {
+            st_stream(p, v);
+        }
     }
 };
 

@@ -665,6 +665,23 @@ struct Stockham {
         }
     }
 
+    // Rows of a row-then-column 2D transform: full C2C rows into y, which the column pass reads
+    // next in place, with plain stores.
+    static void c2c_rows(const cf32* x, cf32* y, int n, int batch, Direction direction,
+                         hipStream_t stream)
+    {
+        const auto rows = static_cast<std::size_t>(batch);
+        if (n == 1 || batch < 1 || (x < y + rows * n && y < x + rows * n)) {
+            c2c_single(x, y, n, batch, direction, stream, n);  // its checks and n = 1 copy
+            return;
+        }
+        check_size(n, "stockham");
+        const bool inverse = direction == Direction::Inverse;
+        const float scale = inverse ? 1.0f / static_cast<float>(n) : 1.0f;
+        dev::dispatch_dir<R, Table>(n, inverse, dev::C2cIo<false, true>{x, y, scale, n, n}, batch,
+                                    stream);
+    }
+
     static void columns(const cf32* x, cf32* y, int n, int cols, int slabs, Direction direction,
                         hipStream_t stream)
     {
@@ -967,6 +984,12 @@ struct Fused2dDriver {
         }
     }
 
+    static void c2c_rows(const cf32* x, cf32* y, int n, int batch, Direction direction,
+                         hipStream_t stream)
+    {
+        Stockham<R, Table>::c2c_rows(x, y, n, batch, direction, stream);
+    }
+
     // The forward's column pass, into the workspace that r2c_rows reads next (plain stores).
     static void r2c_columns(const cf32* x, cf32* z, int n1, int m, int batch, hipStream_t stream)
     {
@@ -989,7 +1012,8 @@ struct Fused2dDriver {
 
     static Fused2dFns fns()
     {
-        return {&supports, &r2c, &c2r, &r2c_columns, &r2c_rows, &c2r_rows, &c2c_supports, &c2c};
+        return {&supports, &r2c,          &c2r, &r2c_columns, &r2c_rows,
+                &c2r_rows, &c2c_supports, &c2c, &c2c_rows};
     }
 
     static void c2r(const cf32* x, float* y, int n1, int n2, int m1, int w, int batch,
