@@ -38,6 +38,11 @@ struct PrunedFns {
     void (*c2r)(const cf32* x, float* y, int n, int batch, int keep, hipStream_t stream);
     void (*columns)(const cf32* x, cf32* y, int n, int cols, int slabs, int m1_in, int m1_out,
                     Direction direction, hipStream_t stream);
+    // r2c and columns into a workspace that the next pass reads (plain stores): the two-pass
+    // rfft2_modes / irfft2_modes.
+    void (*r2c_work)(const float* x, cf32* y, int n, int batch, int keep, hipStream_t stream);
+    void (*columns_work)(const cf32* x, cf32* y, int n, int cols, int slabs, int m1_in,
+                         int m1_out, Direction direction, hipStream_t stream);
 };
 
 // Single-pass 2D real transforms for the shapes whose half spectrum fits in LDS (fft2_fused.hpp):

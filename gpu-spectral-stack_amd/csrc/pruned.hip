@@ -198,7 +198,7 @@ void rfft2_modes(const FftImpl& impl, const float* x, cf32* modes, int n1, int n
         return;
     }
     if (impl.pruned != nullptr) {
-        impl.pruned->r2c(x, work, n2, batch * n1, m2, stream);  // n1 x m2 per array
+        impl.pruned->r2c_work(x, work, n2, batch * n1, m2, stream);  // n1 x m2 per array
         impl.pruned->columns(work, modes, n1, m2, batch, 0, m1, Direction::Forward, stream);
         return;
     }
@@ -229,7 +229,7 @@ void irfft2_modes(const FftImpl& impl, const cf32* modes, float* y, int n1, int 
         return;
     }
     if (impl.pruned != nullptr) {
-        impl.pruned->columns(modes, work, n1, m2, batch, m1, 0, Direction::Inverse, stream);
+        impl.pruned->columns_work(modes, work, n1, m2, batch, m1, 0, Direction::Inverse, stream);
         impl.pruned->c2r(work, y, n2, batch * n1, m2, stream);  // columns m2.. are zero
         return;
     }

@@ -841,7 +841,8 @@ struct C2cIo {
 // so one twiddle serves bins k and m-k (k = 0 pairs with m, whose Z index wraps to 0). This is the
 // split formula of the reference's real.cuh:7-42, evaluated per pair instead of per bin.
 // keep: values per row of y, m + 1 for the whole half spectrum, fewer when pruned.
-struct R2cIo {
+template <bool PlainOut>
+struct R2cIoT {
     static constexpr bool kGroupIsBlock = false;
     static constexpr bool kFinal = true;
     const cf32* z;  // x viewed as complex
@@ -926,11 +927,11 @@ struct R2cIo {
                         constexpr int e = decltype(ei)::value;
                         constexpr int off = (e / RL) * P::L + (e % RL) * (P::N / RL);
                         if (lane + off < keep) {
-                            st_stream(dst + lane + off, v[e]);
+                            put(dst + lane + off, v[e]);
                         }
                     });
                     if (lane == 0 && m < keep) {
-                        st_stream(dst + m, xm);
+                        put(dst + m, xm);
                     }
                 }
             } else {
@@ -978,11 +979,22 @@ struct R2cIo {
         cf32* dst = y + first * keep;
         H::each(count, tid, [&](int, int u, int i, bool valid) {
             if (valid && i < keep) {
-                st_stream(dst + u * keep + i, lds[u * P::kStride + pad(i)]);
+                put(dst + u * keep + i, lds[u * P::kStride + pad(i)]);
             }
         });
     }
+
+    // PlainOut: plain stores, for a workspace that the next pass reads (nontemporal otherwise).
+    __device__ __forceinline__ static void put(cf32* p, cf32 v)
+    {
+        if constexpr (PlainOut) {
+            *p = v;
+        } else {
+            st_stream(p, v);
+        }
+    }
 };
+using R2cIo = R2cIoT<false>;
 
 // Real output (inverse). Rows of x hold X[0 .. keep-1] of the m + 1 half-spectrum values (the
 // rest zero). The load prepares pairs (reference real.cuh:44-61, per pair):

@@ -688,7 +688,9 @@ struct Stockham {
         columns_impl(x, y, n, cols, slabs, direction, stream, 0, 0);
     }
 
-    static void r2c_impl(const float* x, cf32* y, int n, int batch, hipStream_t stream, int keep)
+    // plain_out: y is a workspace that the next pass reads (plain stores).
+    static void r2c_impl(const float* x, cf32* y, int n, int batch, hipStream_t stream, int keep,
+                         bool plain_out = false)
     {
         check_keep(keep, n, "stockham r2c");
         check_real_arguments(x, y, n, batch, keep, 2 * kStockhamMaxN, "stockham r2c");
@@ -698,7 +700,11 @@ struct Stockham {
             r2c_n2(x, y, batch, keep, stream);
             return;
         }
-        dev::dispatch_dir<R, Table>(m, false, dev::R2cIo{z, y, keep}, batch, stream);
+        if (plain_out) {
+            dev::dispatch_dir<R, Table>(m, false, dev::R2cIoT<true>{z, y, keep}, batch, stream);
+        } else {
+            dev::dispatch_dir<R, Table>(m, false, dev::R2cIo{z, y, keep}, batch, stream);
+        }
     }
 
     static void c2r_impl(const cf32* x, float* y, int n, int batch, hipStream_t stream, int keep)
@@ -752,11 +758,26 @@ struct Stockham {
         columns_impl(x, y, n, cols, slabs, direction, stream, m1_in, m1_out);
     }
 
+    // The same two into a workspace that the next pass reads: plain stores.
+    static void pruned_r2c_work(const float* x, cf32* y, int n, int batch, int keep,
+                                hipStream_t stream)
+    {
+        r2c_impl(x, y, n, batch, stream, keep, true);
+    }
+
+    static void pruned_columns_work(const cf32* x, cf32* y, int n, int cols, int slabs,
+                                    int m1_in, int m1_out, Direction direction,
+                                    hipStream_t stream)
+    {
+        columns_impl(x, y, n, cols, slabs, direction, stream, m1_in, m1_out, false);
+    }
+
     // Not constexpr on purpose: a constant-initialized table of host function addresses would
     // also be emitted for the device, where those functions do not exist.
     static PrunedFns pruned_fns()
     {
-        return {&pruned_c2c, &pruned_r2c, &pruned_c2r, &pruned_columns};
+        return {&pruned_c2c,     &pruned_r2c,      &pruned_c2r,
+                &pruned_columns, &pruned_r2c_work, &pruned_columns_work};
     }
 };
 
