@@ -15,8 +15,9 @@ roofline     the forward C2C kernel alone: the same algorithmic bytes per launch
 cpu_baseline numpy.fft (pocketfft, single thread) on the same kind of complex64 input, forward +
              inverse, on a bounded sample of the workload, in the same GB/s convention.
 extra        secondary rows of the metric, each with rocFFT (torch.fft) on the same shape: C2
-             R2C / C2R at n = 1024, C3 rfft2 / irfft2 at 128^2 x 1024 and 512^2 x 64, C4 pruned
-             rfft2 / irfft2 on [64, 32, 128, 128] with m1 = m2 = 16 (ms and effective GB/s);
+             R2C / C2R at n = 1024, C3 rfft2 / irfft2 at 128^2 x 1024 and 512^2 x 64 (columns
+             strided and transpose), C4 pruned rfft2 / irfft2 on [64, 32, 128, 128] with
+             m1 = m2 = 16 (ms and effective GB/s);
              C5 the Navier-Stokes solver on 128^2 x 256 trajectories, 32 frames 40 steps apart,
              fused (this stack's default for the pruned layout) next to this stack's composed
              pruned path, rocFFT pruned and rocFFT full (ms per step and trajectory-steps / s);
@@ -286,7 +287,8 @@ def main(argv=None) -> int:
 
 def secondary_rows(impl: str, dev) -> dict:
     """The other configurations of the metric, each next to rocFFT (through torch.fft) on the same
-    shape: C2 real transforms at n = 1024, C3 rfft2 / irfft2 at 128^2 x 1024 and 512^2 x 64, C4
+    shape: C2 real transforms at n = 1024, C3 rfft2 / irfft2 at 128^2 x 1024 and 512^2 x 64 (both
+    column methods: strided, the default, and transpose), C4
     pruned transforms on [64, 32, 128, 128] with m1 = m2 = 16, and rocFFT on the C1 shape. Inputs
     rotate over three sets so no call reads what the previous one left in the cache."""
     import torch
@@ -325,10 +327,18 @@ def secondary_rows(impl: str, dev) -> dict:
         xs = [torch.randn(arrays, n, n, device=dev, generator=g) for _ in range(3)]
         hs = [torch.fft.rfft2(x) for x in xs]
         work = fft2_real_work(n, n, arrays)[1]
-        record(f"c3_rfft2_{n}", timed(lambda x: spectral.rfft2(x, impl=impl), xs), work,
-               timed(torch.fft.rfft2, xs))
+        roc_f = timed(torch.fft.rfft2, xs)
+        roc_i = timed(lambda x: torch.fft.irfft2(x, s=(n, n)), hs)
+        record(f"c3_rfft2_{n}", timed(lambda x: spectral.rfft2(x, impl=impl), xs), work, roc_f)
         record(f"c3_irfft2_{n}", timed(lambda x: spectral.irfft2(x, n, impl=impl), hs), work,
-               timed(lambda x: torch.fft.irfft2(x, s=(n, n)), hs))
+               roc_i)
+        # BASELINE C3's second variant: the transpose method (rows, transpose, rows, transpose).
+        record(f"c3_rfft2_{n}_transpose",
+               timed(lambda x: spectral.rfft2(x, impl=impl, columns="transpose"), xs), work,
+               roc_f)
+        record(f"c3_irfft2_{n}_transpose",
+               timed(lambda x: spectral.irfft2(x, n, impl=impl, columns="transpose"), hs), work,
+               roc_i)
         del xs, hs
     # C4: FNO pruned transforms, [64, 32, 128, 128] <-> modes [64, 32, 32, 16].
     xp = [torch.randn(64, 32, 128, 128, device=dev, generator=g) for _ in range(3)]

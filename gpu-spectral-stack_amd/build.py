@@ -59,6 +59,7 @@ CAPI_SOURCES = [
     "real.hip",
     "naive.hip",
     "scale.hip",
+    "remap.hip",
     "fft2d.hip",
     "pruned.hip",
     "ns.hip",

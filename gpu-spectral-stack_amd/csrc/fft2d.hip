@@ -1,12 +1,21 @@
-// Two-dimensional FFTs from the 1D kernels (reference fft2d.hpp:3-16, fft2d.cu:15-187): rows
-// first, then the columns either in place with the strided column kernel ("strided"), or by
-// transposing, running rows, and transposing back ("transpose", every implementation). Real
-// transforms keep n2/2 + 1 columns on the complex side. Forward unnormalized; the inverse divides
-// by n1 * n2, split between the two passes (1/n2 in the rows, 1/n1 in the columns).
+// Two-dimensional FFTs over the last two axes of batch arrays of n1 x n2 (the contract of
+// reference fft2d.hpp:3-16: rows then columns, real transforms keep n2/2 + 1 columns on the
+// complex side, forward unnormalized, inverse divided by n1 n2).
 //
-// The transpose is an LDS-tiled 64 x 64 copy sized for wave64: each wavefront reads one tile row
-// of 64 complex values (512 contiguous bytes) and writes one transposed row, through a tile padded
-// to 65 columns so the column-order LDS reads fall in distinct banks.
+// A request is planned once (plan_2d): the route it takes and the workspace that route needs.
+// The workspace queries return the plan's size and the transforms run the plan's route, so the
+// two agree by construction. Routes, best first for the strided method:
+//
+//   SinglePass        the whole array in one workgroup's LDS, one kernel (fft2_fused.hpp)
+//   ColumnFirst       real transforms from n2 = 32: columns of the real array read as complex,
+//                     then one pass over row pairs (k1, -k1) (fft2_pairs.hpp); no misaligned
+//                     half-spectrum rows in the column pass
+//   RowsThenColumns   row kernel, then the strided column kernel in place (or, for the
+//                     inverse real transform, columns out of place then the real rows)
+//   Transposes        the "transpose" method, every implementation: rows, a transpose, the
+//                     columns as contiguous rows, a transpose back (remap.hip's tiled kernel)
+//
+// The inverse's 1 / (n1 n2) comes from the 1D passes: 1/n2 in the rows, 1/n1 in the columns.
 
 #include "fft_api.hpp"
 
@@ -16,50 +25,34 @@
 namespace spx {
 namespace {
 
-constexpr int kTile = 64;
-constexpr int kTileRows = 4;  // 64 x 4 lanes move a 64 x 64 tile in 16 steps
+enum class Kind { C2c, R2c, C2r };
+enum class Route { SinglePass, ColumnFirst, RowsThenColumns, Transposes };
 
-__global__ void __launch_bounds__(kTile * kTileRows)
-    transpose_kernel(const cf32* __restrict__ x, cf32* __restrict__ y, int rows, int cols,
-                     int batch)
-{
-    __shared__ cf32 tile[kTile][kTile + 1];
-    const std::size_t size = static_cast<std::size_t>(rows) * static_cast<std::size_t>(cols);
-    const int tx = threadIdx.x;  // 0 .. 63
-    const int ty = threadIdx.y;  // 0 .. 3
-    for (int b = blockIdx.z; b < batch; b += gridDim.z) {
-        const cf32* xs = x + static_cast<std::size_t>(b) * size;
-        cf32* ys = y + static_cast<std::size_t>(b) * size;
-        const int c = blockIdx.x * kTile + tx;
-#pragma unroll
-        for (int k = 0; k < kTile; k += kTileRows) {
-            const int r = blockIdx.y * kTile + ty + k;
-            if (r < rows && c < cols) {
-                tile[ty + k][tx] = xs[static_cast<std::size_t>(r) * cols + c];
-            }
-        }
-        __syncthreads();
-        const int r_out = blockIdx.y * kTile + tx;  // a row of y is a column of x
-#pragma unroll
-        for (int k = 0; k < kTile; k += kTileRows) {
-            const int c_out = blockIdx.x * kTile + ty + k;
-            if (r_out < rows && c_out < cols) {
-                ys[static_cast<std::size_t>(c_out) * rows + r_out] = tile[tx][ty + k];
-            }
-        }
-        __syncthreads();  // the tile is reused for the next array
+struct Plan2d {
+    Route route;
+    int n1;
+    int n2;
+    int batch;
+    int regions;         // array-sized workspace regions the route passes through (0 .. 2)
+    std::size_t region;  // cf32 values per region
+    std::size_t real;    // scratch of the generic real rows (implementations that need it)
+
+    std::size_t words() const { return static_cast<std::size_t>(regions) * region + real; }
+    cf32* at(cf32* work, int i) const { return work + static_cast<std::size_t>(i) * region; }
+    cf32* real_scratch(cf32* work) const
+    {
+        return real > 0 ? work + static_cast<std::size_t>(regions) * region : nullptr;
     }
-}
+};
 
-std::size_t count(int n1, int n2, int batch)
+std::size_t values(int rows, int cols, int batch)
 {
-    return static_cast<std::size_t>(batch) * static_cast<std::size_t>(n1)
-           * static_cast<std::size_t>(n2);
+    return static_cast<std::size_t>(batch) * static_cast<std::size_t>(rows)
+           * static_cast<std::size_t>(cols);
 }
 
-// Throws unless the shape suits the implementation, the method exists, and every intermediate
-// transform count fits an int (reference fft2d.cu:100-128, same messages).
-void check(const FftImpl& impl, Columns columns, int n1, int n2, int batch, bool real)
+// The shape checks and their messages are the reference's API (fft2d.cu:100-128).
+void validate(const FftImpl& impl, Columns columns, int n1, int n2, int batch, bool real)
 {
     const std::string name = impl.name;
     const int max_n2 = real ? impl.max_real_n : impl.max_n;
@@ -84,25 +77,48 @@ void check(const FftImpl& impl, Columns columns, int n1, int n2, int batch, bool
     }
 }
 
-std::size_t real_work(const FftImpl& impl, int n1, int n2, int batch)
+Plan2d plan_2d(const FftImpl& impl, Columns columns, Kind kind, int n1, int n2, int batch)
 {
-    return impl.real_needs_work ? count(n1, n2 / 2, batch) : 0;
+    validate(impl, columns, n1, n2, batch, kind != Kind::C2c);
+    Plan2d p{Route::Transposes, n1, n2, batch, 0, 0, 0};
+    const int w = kind == Kind::C2c ? n2 : n2 / 2 + 1;
+    const std::size_t real_rows =
+        kind != Kind::C2c && impl.real_needs_work ? values(n1, n2 / 2, batch) : 0;
+    if (columns == Columns::Transpose) {
+        p.regions = 2;
+        p.region = values(n1, w, batch);
+        p.real = real_rows;
+        return p;
+    }
+    const Fused2dFns* f = impl.fused;
+    if (kind == Kind::C2c) {
+        p.route = f != nullptr && f->c2c_supports(n1, n2) ? Route::SinglePass
+                                                          : Route::RowsThenColumns;
+        return p;
+    }
+    if (f != nullptr && f->supports(n1, n2)) {
+        p.route = Route::SinglePass;
+    } else if (f != nullptr && n2 >= 32) {
+        p.route = Route::ColumnFirst;
+        p.regions = 1;
+        p.region = values(n1, n2 / 2, batch);
+    } else {
+        p.route = Route::RowsThenColumns;
+        p.real = real_rows;
+        if (kind == Kind::C2r) {  // columns out of place: the input is the caller's
+            p.regions = 1;
+            p.region = values(n1, w, batch);
+        }
+    }
+    return p;
 }
 
-// The strided method runs as one single-pass kernel when the implementation has one for the shape.
-bool fused(const FftImpl& impl, Columns columns, int n1, int n2)
+// batch arrays of rows x cols -> cols x rows
+void transpose_arrays(const cf32* x, cf32* y, int rows, int cols, int batch, hipStream_t stream)
 {
-    return columns == Columns::Strided && impl.fused != nullptr && impl.fused->supports(n1, n2);
-}
-
-// Otherwise, from n2 = 32, column-first (fft2_pairs.hpp): columns over the real array read as
-// n1 x n2/2 complex values, whose rows are whole 128-byte lines, and one row-pair pass on the
-// other side; the row-then-column order would run its column pass over half-spectrum rows of
-// n2/2 + 1 values, misaligned.
-bool column_first(const FftImpl& impl, Columns columns, int n1, int n2)
-{
-    return columns == Columns::Strided && impl.fused != nullptr && !impl.fused->supports(n1, n2)
-           && n2 >= 32;
+    const Remap r{cols, rows, cols, static_cast<long long>(rows) * cols, batch,
+                  AxisMap::identity(rows), AxisMap::identity(cols)};
+    remap(x, y, r, true, stream);
 }
 
 }  // namespace
@@ -112,28 +128,34 @@ void transpose(const cf32* x, cf32* y, int rows, int cols, int batch, hipStream_
     if (rows < 1 || cols < 1 || batch < 1) {
         throw InvalidArgument("transpose: need rows, cols, batch >= 1");
     }
-    const dim3 block(kTile, kTileRows);
-    const dim3 grid(static_cast<unsigned>((cols + kTile - 1) / kTile),
-                    static_cast<unsigned>((rows + kTile - 1) / kTile),
-                    static_cast<unsigned>(std::min(batch, 65535)));
-    hipLaunchKernelGGL(transpose_kernel, grid, block, 0, stream, x, y, rows, cols, batch);
-    SPX_LAUNCH_CHECK();
+    transpose_arrays(x, y, rows, cols, batch, stream);
 }
 
-std::size_t fft2_c2c_workspace(const FftImpl&, Columns columns, int n1, int n2, int batch)
+std::size_t fft2_c2c_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch)
 {
-    return columns == Columns::Strided ? 0 : 2 * count(n1, n2, batch);
+    return plan_2d(impl, columns, Kind::C2c, n1, n2, batch).words();
+}
+
+std::size_t fft2_r2c_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch)
+{
+    return plan_2d(impl, columns, Kind::R2c, n1, n2, batch).words();
+}
+
+std::size_t fft2_c2r_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch)
+{
+    return plan_2d(impl, columns, Kind::C2r, n1, n2, batch).words();
 }
 
 void fft2_c2c(const FftImpl& impl, Columns columns, const cf32* x, cf32* y, int n1, int n2,
               int batch, Direction direction, cf32* work, hipStream_t stream)
 {
-    check(impl, columns, n1, n2, batch, false);
-    if (columns == Columns::Strided && impl.fused != nullptr && impl.fused->c2c_supports(n1, n2)) {
+    const Plan2d p = plan_2d(impl, columns, Kind::C2c, n1, n2, batch);
+    switch (p.route) {
+    case Route::SinglePass:
         impl.fused->c2c(x, y, n1, n2, batch, direction, stream);
         return;
-    }
-    if (columns == Columns::Strided) {
+    case Route::RowsThenColumns:
+        // The row pass writes y, which the column pass then transforms in place.
         if (impl.fused != nullptr) {
             impl.fused->c2c_rows(x, y, n2, batch * n1, direction, stream);
         } else {
@@ -141,97 +163,76 @@ void fft2_c2c(const FftImpl& impl, Columns columns, const cf32* x, cf32* y, int 
         }
         impl.columns(y, y, n1, n2, batch, direction, stream);
         return;
+    default: {
+        cf32* a = p.at(work, 0);
+        cf32* b = p.at(work, 1);
+        impl.c2c(x, a, n2, batch * n1, direction, stream);
+        transpose_arrays(a, b, n1, n2, batch, stream);
+        impl.c2c(b, a, n1, batch * n2, direction, stream);
+        transpose_arrays(a, y, n2, n1, batch, stream);
+        return;
     }
-    cf32* a = work;
-    cf32* b = work + count(n1, n2, batch);
-    impl.c2c(x, a, n2, batch * n1, direction, stream);
-    transpose(a, b, n1, n2, batch, stream);
-    impl.c2c(b, a, n1, batch * n2, direction, stream);
-    transpose(a, y, n2, n1, batch, stream);
-}
-
-std::size_t fft2_r2c_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch)
-{
-    if (fused(impl, columns, n1, n2)) {
-        return 0;
     }
-    if (column_first(impl, columns, n1, n2)) {
-        return count(n1, n2 / 2, batch);
-    }
-    const std::size_t half = columns == Columns::Strided ? 0 : 2 * count(n1, n2 / 2 + 1, batch);
-    return half + real_work(impl, n1, n2, batch);
 }
 
 void fft2_r2c(const FftImpl& impl, Columns columns, const float* x, cf32* y, int n1, int n2,
               int batch, cf32* work, hipStream_t stream)
 {
-    check(impl, columns, n1, n2, batch, true);
+    const Plan2d p = plan_2d(impl, columns, Kind::R2c, n1, n2, batch);
     const int w = n2 / 2 + 1;
-    if (fused(impl, columns, n1, n2)) {
+    switch (p.route) {
+    case Route::SinglePass:
         impl.fused->r2c(x, y, n1, n2, 0, w, batch, stream);
         return;
-    }
-    if (column_first(impl, columns, n1, n2)) {
-        impl.fused->r2c_columns(reinterpret_cast<const cf32*>(x), work, n1, n2 / 2, batch, stream);
-        impl.fused->r2c_rows(work, y, n1, n2 / 2, batch, stream);
+    case Route::ColumnFirst:
+        impl.fused->r2c_columns(reinterpret_cast<const cf32*>(x), p.at(work, 0), n1, n2 / 2,
+                                batch, stream);
+        impl.fused->r2c_rows(p.at(work, 0), y, n1, n2 / 2, batch, stream);
         return;
-    }
-    if (columns == Columns::Strided) {
-        cf32* rwork = impl.real_needs_work ? work : nullptr;
-        impl.r2c(x, y, n2, batch * n1, rwork, stream);
+    case Route::RowsThenColumns:
+        impl.r2c(x, y, n2, batch * n1, p.real_scratch(work), stream);
         impl.columns(y, y, n1, w, batch, Direction::Forward, stream);
         return;
+    default: {
+        cf32* a = p.at(work, 0);
+        cf32* b = p.at(work, 1);
+        impl.r2c(x, a, n2, batch * n1, p.real_scratch(work), stream);
+        transpose_arrays(a, b, n1, w, batch, stream);
+        impl.c2c(b, a, n1, batch * w, Direction::Forward, stream);
+        transpose_arrays(a, y, w, n1, batch, stream);
+        return;
     }
-    cf32* a = work;
-    cf32* b = work + count(n1, w, batch);
-    cf32* rwork = impl.real_needs_work ? work + 2 * count(n1, w, batch) : nullptr;
-    impl.r2c(x, a, n2, batch * n1, rwork, stream);
-    transpose(a, b, n1, w, batch, stream);
-    impl.c2c(b, a, n1, batch * w, Direction::Forward, stream);
-    transpose(a, y, w, n1, batch, stream);
-}
-
-std::size_t fft2_c2r_workspace(const FftImpl& impl, Columns columns, int n1, int n2, int batch)
-{
-    if (fused(impl, columns, n1, n2)) {
-        return 0;
     }
-    const std::size_t q = count(n1, n2 / 2 + 1, batch);
-    return (columns == Columns::Strided ? q : 2 * q) + real_work(impl, n1, n2, batch);
 }
 
 void fft2_c2r(const FftImpl& impl, Columns columns, const cf32* x, float* y, int n1, int n2,
               int batch, cf32* work, hipStream_t stream)
 {
-    check(impl, columns, n1, n2, batch, true);
+    const Plan2d p = plan_2d(impl, columns, Kind::C2r, n1, n2, batch);
     const int w = n2 / 2 + 1;
-    if (fused(impl, columns, n1, n2)) {
+    switch (p.route) {
+    case Route::SinglePass:
         impl.fused->c2r(x, y, n1, n2, 0, w, batch, stream);
         return;
-    }
-    if (column_first(impl, columns, n1, n2)) {
-        // The workspace holds n1 x (n2/2 + 1) per array, more than the n1 x n2/2 used here.
-        impl.fused->c2r_rows(x, work, n1, n2 / 2, batch, stream);
-        impl.columns(work, reinterpret_cast<cf32*>(y), n1, n2 / 2, batch, Direction::Inverse,
-                     stream);
+    case Route::ColumnFirst:
+        impl.fused->c2r_rows(x, p.at(work, 0), n1, n2 / 2, batch, stream);
+        impl.columns(p.at(work, 0), reinterpret_cast<cf32*>(y), n1, n2 / 2, batch,
+                     Direction::Inverse, stream);
+        return;
+    case Route::RowsThenColumns:
+        impl.columns(x, p.at(work, 0), n1, w, batch, Direction::Inverse, stream);
+        impl.c2r(p.at(work, 0), y, n2, batch * n1, p.real_scratch(work), stream);
+        return;
+    default: {
+        cf32* a = p.at(work, 0);
+        cf32* b = p.at(work, 1);
+        transpose_arrays(x, a, n1, w, batch, stream);
+        impl.c2c(a, b, n1, batch * w, Direction::Inverse, stream);
+        transpose_arrays(b, a, w, n1, batch, stream);
+        impl.c2r(a, y, n2, batch * n1, p.real_scratch(work), stream);
         return;
     }
-    const std::size_t q = count(n1, w, batch);
-    if (columns == Columns::Strided) {
-        // Columns first, out of place (the input is the caller's), then the real rows.
-        cf32* a = work;
-        cf32* rwork = impl.real_needs_work ? work + q : nullptr;
-        impl.columns(x, a, n1, w, batch, Direction::Inverse, stream);
-        impl.c2r(a, y, n2, batch * n1, rwork, stream);
-        return;
     }
-    cf32* a = work;
-    cf32* b = work + q;
-    cf32* rwork = impl.real_needs_work ? work + 2 * q : nullptr;
-    transpose(x, a, n1, w, batch, stream);
-    impl.c2c(a, b, n1, batch * w, Direction::Inverse, stream);
-    transpose(b, a, w, n1, batch, stream);
-    impl.c2r(a, y, n2, batch * n1, rwork, stream);
 }
 
 }  // namespace spx

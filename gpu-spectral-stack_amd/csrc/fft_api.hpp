@@ -121,6 +121,54 @@ void c2r_via_c2c(C2cFn c2c, const cf32* x, float* y, int n, int batch, cf32* wor
 // --- scale (scale.hip) ----------------------------------------------------------------------
 void scale_c2c(const cf32* x, cf32* y, std::size_t n, float alpha, hipStream_t stream);
 
+// --- index remaps (remap.hip): transposes, mode gathers and mode scatters ---------------------
+//
+// Where output index i along one axis reads along the input axis, or -1 for a zero:
+//   Identity  i -> i while i < limit
+//   Keep      kept position -> full position, the FNO rows: i < m1 ? i : i + n - 2 m1
+//             (m1 = 0 keeps every position: i -> i while i < n)
+//   Spread    full position -> kept position, the inverse of Keep (-1 for a dropped one),
+//             and -1 past `limit` kept positions when the axis is narrowed
+struct AxisMap {
+    enum Kind : int { Identity, Keep, Spread };
+    Kind kind;
+    int n;
+    int m1;
+    int limit;
+
+    static AxisMap identity(int limit) { return {Identity, limit, 0, limit}; }
+    static AxisMap keep(int n, int m1) { return {Keep, n, m1, m1 > 0 ? 2 * m1 : n}; }
+    static AxisMap spread(int n, int m1) { return {Spread, n, m1, n}; }
+
+    __host__ __device__ int operator()(int i) const
+    {
+        if (kind == Identity) {
+            return i < limit ? i : -1;
+        }
+        if (kind == Keep) {
+            return m1 == 0 || i < m1 ? i : i + n - 2 * m1;
+        }
+        if (m1 == 0 || i < m1) {
+            return i < limit ? i : -1;
+        }
+        return i >= n - m1 ? i - n + 2 * m1 : -1;
+    }
+};
+
+// batch arrays: y (y_rows x y_cols per array, dense) from x (x_array values per array, rows of
+// x_pitch). Not transposed: y[q][p] = x[rows(q)][cols(p)]. Transposed: y[q][p] = x[rows(p)][cols(q)].
+// A -1 from either map writes a zero, so a scatter fills the whole output in the same pass.
+struct Remap {
+    int y_rows;
+    int y_cols;
+    long long x_pitch;
+    long long x_array;
+    int batch;
+    AxisMap rows;
+    AxisMap cols;
+};
+void remap(const cf32* x, cf32* y, const Remap& r, bool transposed, hipStream_t stream);
+
 // --- 2D (fft2d.hip), reference fft2d.hpp:24-39 -----------------------------------------------
 enum class Columns { Transpose, Strided };
 

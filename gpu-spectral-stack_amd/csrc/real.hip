@@ -85,6 +85,35 @@ const cf32* twiddle_table()
     return table;
 }
 
+bool pool_retained()
+{
+    // Decided once per device: 1 retained, 2 no memory pools.
+    static std::mutex mutex;
+    static std::vector<unsigned char> state;
+
+    int device = 0;
+    SPX_HIP_CHECK(hipGetDevice(&device));
+    const std::lock_guard<std::mutex> lock(mutex);
+    if (state.size() <= static_cast<std::size_t>(device)) {
+        state.resize(static_cast<std::size_t>(device) + 1, 0);
+    }
+    unsigned char& s = state[static_cast<std::size_t>(device)];
+    if (s == 0) {
+        int pools = 0;
+        SPX_HIP_CHECK(hipDeviceGetAttribute(&pools, hipDeviceAttributeMemoryPoolsSupported,
+                                            device));
+        if (pools != 0) {
+            hipMemPool_t pool = nullptr;
+            SPX_HIP_CHECK(hipDeviceGetDefaultMemPool(&pool, device));
+            std::uint64_t keep_everything = UINT64_MAX;
+            SPX_HIP_CHECK(
+                hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep_everything));
+        }
+        s = pools != 0 ? 1 : 2;
+    }
+    return s == 1;
+}
+
 namespace {
 
 constexpr int kThreads = 256;

@@ -1,0 +1,141 @@
+// Index remaps: one pass that copies batch arrays through a row map and a column map, either in
+// the same orientation or transposed. It is the transpose of the 2D "transpose" method and of the
+// four-step, the gather of FNO modes out of a full half spectrum, and the scatter back (whose
+// zeros it writes in the same pass: every output value is written exactly once).
+//
+// Design for gfx950 (wave64, LDS of 64 banks of 4 bytes, read by half-waves for 8-byte values):
+//
+// * Transposed: a workgroup of four waves moves a 64 x 64 tile of complex values. A wave reads
+//   one input row segment per step (64 lanes x 8 bytes, 512 contiguous bytes), holds all 16 of
+//   its steps' loads in registers before touching LDS (every load in flight together), then
+//   writes them to the tile; after one barrier it reads tile columns and writes output rows,
+//   again 512 contiguous bytes per wave step.
+//   The tile is unpadded and XOR-swizzled: element (p, q) sits at p * 64 + (q ^ (p mod 32)).
+//   A half-wave writing a row (fixed p, 32 consecutive q) and a half-wave reading a column
+//   (fixed q, 32 consecutive p) both cover 32 distinct 8-byte bank slots, so neither phase has a
+//   bank conflict, and the tile needs no padding column (32 KiB, five workgroups per CU).
+// * Not transposed: each output row is walked by a power-of-two group of lanes as wide as the row
+//   (up to a wave), so short rows (16 modes) still fill whole waves with several rows each. The
+//   row and column maps are evaluated per lane; no flat-index division per value.
+
+#include "fft_api.hpp"
+
+#include <algorithm>
+
+namespace spx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 64;
+constexpr int kSteps = kTile / (kThreads / 64);  // tile rows per wave: 16
+constexpr long long kMaxBlocks = 1 << 20;        // the loops below cover any remainder
+
+__device__ __forceinline__ cf32 zero() { return cf32{0.0f, 0.0f}; }
+
+__global__ void __launch_bounds__(kThreads)
+    remap_tiles_kernel(const cf32* __restrict__ x, cf32* __restrict__ y, Remap r, int tiles_p,
+                       int tiles_q, long long tiles)
+{
+    __shared__ cf32 tile[kTile * kTile];
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const long long per_array = static_cast<long long>(tiles_p) * tiles_q;
+    for (long long t = blockIdx.x; t < tiles; t += gridDim.x) {
+        const long long b = t / per_array;
+        const int rest = static_cast<int>(t - b * per_array);
+        const int tq = rest / tiles_p;
+        const int p0 = (rest - tq * tiles_p) * kTile;  // output columns = input rows
+        const int q0 = tq * kTile;                      // output rows = input columns
+        const cf32* xs = x + b * r.x_array;
+
+        // Input row rows(p) at column cols(q): lane -> q, wave + 4 k -> p.
+        const int q_in = q0 + lane;
+        const int xc = q_in < r.y_rows ? r.cols(q_in) : -1;
+        cf32 v[kSteps];
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            const int p = p0 + wave + 4 * k;
+            const int xr = p < r.y_cols ? r.rows(p) : -1;
+            v[k] = (xr >= 0 && xc >= 0) ? xs[static_cast<long long>(xr) * r.x_pitch + xc] : zero();
+        }
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            const int pl = wave + 4 * k;
+            tile[pl * kTile + (lane ^ (pl & 31))] = v[k];
+        }
+        __syncthreads();
+        // Output row q0 + wave + 4 k, column p0 + lane: tile column, read across p.
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            const int ql = wave + 4 * k;
+            v[k] = tile[lane * kTile + (ql ^ (lane & 31))];
+        }
+        cf32* ys = y + b * static_cast<long long>(r.y_rows) * r.y_cols;
+        const int p_out = p0 + lane;
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+            const int q = q0 + wave + 4 * k;
+            if (q < r.y_rows && p_out < r.y_cols) {
+                ys[static_cast<long long>(q) * r.y_cols + p_out] = v[k];
+            }
+        }
+        __syncthreads();  // the next tile overwrites the LDS
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+    remap_rows_kernel(const cf32* __restrict__ x, cf32* __restrict__ y, Remap r, int lanes_log2,
+                      long long total_rows)
+{
+    const int lanes = 1 << lanes_log2;
+    const int sub = static_cast<int>(threadIdx.x) >> lanes_log2;  // row within the workgroup
+    const int lane = static_cast<int>(threadIdx.x) & (lanes - 1);
+    const int rows_per_block = kThreads >> lanes_log2;
+    for (long long row = static_cast<long long>(blockIdx.x) * rows_per_block + sub;
+         row < total_rows; row += static_cast<long long>(gridDim.x) * rows_per_block) {
+        const long long b = row / r.y_rows;
+        const int xr = r.rows(static_cast<int>(row - b * r.y_rows));
+        cf32* ys = y + row * r.y_cols;
+        if (xr < 0) {
+            for (int p = lane; p < r.y_cols; p += lanes) {
+                ys[p] = zero();
+            }
+            continue;
+        }
+        const cf32* xs = x + b * r.x_array + static_cast<long long>(xr) * r.x_pitch;
+        for (int p = lane; p < r.y_cols; p += lanes) {
+            const int xc = r.cols(p);
+            ys[p] = xc >= 0 ? xs[xc] : zero();
+        }
+    }
+}
+
+unsigned blocks(long long work) { return static_cast<unsigned>(std::min(work, kMaxBlocks)); }
+
+}  // namespace
+
+void remap(const cf32* x, cf32* y, const Remap& r, bool transposed, hipStream_t stream)
+{
+    if (r.y_rows < 1 || r.y_cols < 1 || r.batch < 1) {
+        throw InvalidArgument("remap: need at least one row, one column and one array");
+    }
+    if (transposed) {
+        const int tiles_p = (r.y_cols + kTile - 1) / kTile;
+        const int tiles_q = (r.y_rows + kTile - 1) / kTile;
+        const long long tiles = static_cast<long long>(tiles_p) * tiles_q * r.batch;
+        hipLaunchKernelGGL(remap_tiles_kernel, dim3(blocks(tiles)), dim3(kThreads), 0, stream, x,
+                           y, r, tiles_p, tiles_q, tiles);
+    } else {
+        int lanes_log2 = 0;
+        while (lanes_log2 < 6 && (1 << lanes_log2) < r.y_cols) {
+            ++lanes_log2;
+        }
+        const long long rows = static_cast<long long>(r.y_rows) * r.batch;
+        const long long per_block = kThreads >> lanes_log2;
+        hipLaunchKernelGGL(remap_rows_kernel, dim3(blocks((rows + per_block - 1) / per_block)),
+                           dim3(kThreads), 0, stream, x, y, r, lanes_log2, rows);
+    }
+    SPX_LAUNCH_CHECK();
+}
+
+}  // namespace spx

@@ -35,6 +35,12 @@ void c2r_n2(const cf32* x, float* y, int batch, int keep, hipStream_t stream);
 bool c2r_n4(const cf32* x, float* y, int batch, int keep, hipStream_t stream);
 // The table of exp(-2 pi i m / kTableN) on the current device, built on first use.
 const cf32* twiddle_table();
+// Whether the current device's default memory pool keeps what is freed into it (its release
+// threshold raised to the maximum on first use), so the stream-ordered workspaces of the large
+// transforms reuse one reservation across calls instead of returning memory to the driver at
+// every synchronization and mapping it again (the reference's fourstep.cu:9-37 policy). False on
+// a device without memory pools: the caller then allocates synchronously.
+bool pool_retained();
 
 namespace dev {
 
@@ -411,16 +417,23 @@ using TransposedRowsPlan = Plan<N, R, cmax(cmax(R, 4), N * 16 / kMaxBlock), kMax
 
 }  // namespace dev
 
-// Stream-ordered scratch memory for one four-step call: allocated on `stream`, freed on it after
-// the kernels queued in between, so no device-wide synchronization is needed.
+// Stream-ordered scratch memory for one large-transform call: allocated on `stream` from the
+// device's retained default pool, freed on it after the kernels queued in between, so no
+// device-wide synchronization is needed. Without memory pools: hipMalloc / hipFree.
 class StreamWorkspace {
 public:
-    StreamWorkspace(std::size_t count, hipStream_t stream) : stream_(stream)
+    StreamWorkspace(std::size_t count, hipStream_t stream)
+        : stream_(stream), pooled_(pool_retained())
     {
-        SPX_HIP_CHECK(hipMallocAsync(reinterpret_cast<void**>(&ptr_), count * sizeof(cf32),
-                                     stream));
+        void* raw = nullptr;
+        if (pooled_) {
+            SPX_HIP_CHECK(hipMallocAsync(&raw, count * sizeof(cf32), stream));
+        } else {
+            SPX_HIP_CHECK(hipMalloc(&raw, count * sizeof(cf32)));
+        }
+        ptr_ = static_cast<cf32*>(raw);
     }
-    ~StreamWorkspace() { (void)hipFreeAsync(ptr_, stream_); }
+    ~StreamWorkspace() { (void)(pooled_ ? hipFreeAsync(ptr_, stream_) : hipFree(ptr_)); }
     StreamWorkspace(const StreamWorkspace&) = delete;
     StreamWorkspace& operator=(const StreamWorkspace&) = delete;
     cf32* get() const { return ptr_; }
@@ -428,6 +441,7 @@ public:
 private:
     cf32* ptr_ = nullptr;
     hipStream_t stream_;
+    bool pooled_;
 };
 
 template <int R, bool Table>

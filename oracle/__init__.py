@@ -15,6 +15,12 @@ Modules:
 Pinning (what makes each function trustworthy, besides the reference's own tests):
   reference.fft/ifft/rfft/irfft/fft2/...  numpy.fft (pocketfft), itself pinned against the O(N^2)
       definition `dft` at small sizes and closed forms (impulse, tone, constant).
+  reference.ifft2  the inverse definition on both axes (conjugate of `dft` applied twice),
+      row-then-column ifft, fft2 round trip, and a separable tone's closed form.
+  reference.fft_truncate  the first k outputs of `dft`; a tone at k - 1 peaks in the last slot.
+  reference.ifft_from_modes  the inverse definition summed over the kept input frequencies one
+      at a time, a unit mode's closed form e^{2 pi i k m / n} / n, and ifft_from_modes(fft(x)) = x.
+      Planted mistakes (modes at the end, forward sign, unscaled) fail these checks.
   reference.rfft2_truncate / irfft2_from_modes  the frequency semantics of the FNO layout,
       pinned by a brute-force enumeration of kept frequencies and the committed fixture
       tests/golden/modes_index.json, and by the reference's own known-answer test

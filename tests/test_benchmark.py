@@ -82,31 +82,6 @@ def test_time_gpu_measures_real_kernel_time():
     assert 100 < gbps < 20000
 
 
-@pytest.mark.gpu
-def test_bench_rf_writes_the_reference_rows(tmp_path):
-    from spectral import bench_rf, rf
-
-    out = tmp_path / "rf.csv"
-    assert bench_rf.main(["--samples", "4096", "--taps", "7", "--nfft", "64",
-                          "--out", str(out)]) == 0
-    rows = [line.split(",") for line in out.read_text().splitlines()
-            if line and not line.startswith("#")]
-    assert rows[0][:5] == ["op", "impl", "n", "batch", "time_ms"]
-    ops = {(r[0], r[1]) for r in rows[1:]}
-    for impl in rf.FFT_BACKENDS:
-        assert ("fir_7", impl) in ops and ("spectrum_64", impl) in ops
-
-
-@pytest.mark.gpu
-def test_bench_torch_writes_one_row_per_size(tmp_path):
-    from spectral import bench_torch
-
-    out = tmp_path / "torch.csv"
-    assert bench_torch.main(["--sizes", "8,64", "--total", "4096", "--out", str(out)]) == 0
-    rows = [line for line in out.read_text().splitlines() if line and not line.startswith("#")]
-    assert len(rows) == 3 and rows[1].startswith("fft_c2c,torch,8,512,")
-
-
 def test_cpu_baseline_reports_its_sample_and_the_wider_rows():
     import bench
 

@@ -139,6 +139,11 @@ def test_workspace_queries(lib):
     assert count.value == 0
     assert lib.spx_fft_c2c_pruned_workspace(0, 64, 8, 3, ctypes.byref(count)) == SPX_OK
     assert count.value == 64 * 3
+    # naive: the real rows' n1 x w, the m2 kept columns' m2 x n1, and its real-row scratch
+    assert lib.spx_rfft2_modes_workspace(0, 64, 32, 4, 5, 3, ctypes.byref(count)) == SPX_OK
+    assert count.value == 3 * (64 * 17 + 5 * 64 + 64 * 16)
+    assert lib.spx_irfft2_modes_workspace(0, 64, 32, 4, 5, 3, ctypes.byref(count)) == SPX_OK
+    assert count.value == 3 * (64 * 17 + 5 * 64 + 64 * 16)
 
 
 @pytest.mark.gpu
@@ -321,3 +326,120 @@ def test_direct_pruned_r2c_at_every_row_width(lib, rng, n):
         assert lib.spx_pruned_r2c(3, _ptr(xd), _ptr(yd), n, batch, keep, None) == SPX_OK
         torch.cuda.synchronize()
         assert_transform_close(yd, full[:, :keep], n)
+
+
+def test_mode_gather_and_scatter_reject_bad_shapes(lib):
+    # Checked on the host before any launch, so these need no GPU: each would otherwise index
+    # outside the arrays.
+    p = ctypes.c_void_p(0x1000)
+    q = ctypes.c_void_p(0x100000)
+    for fn in (lib.spx_gather_modes, lib.spx_scatter_modes):
+        name = "gather_modes" if fn is lib.spx_gather_modes else "scatter_modes"
+        # (n1, w, m1, m2, batch)
+        for bad in [(8, 5, 2, 3, -1), (8, 5, 2, 3, 0), (0, 5, 1, 3, 1), (8, 0, 1, 1, 1),
+                    (8, 5, -1, 3, 1), (8, 5, 5, 3, 1), (8, 5, 2, 0, 1), (8, 5, 2, -2, 1),
+                    (8, 5, 2, 6, 1)]:
+            assert fn(p, q, *bad, None) == SPX_EINVAL, bad
+            assert name in _last(lib), (bad, _last(lib))
+
+
+def _golden_cases():
+    import json
+
+    return json.loads((REPO / "tests" / "golden" / "modes_index.json").read_text())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", _golden_cases(), ids=lambda c: f"{c['n1']}x{c['n2']}-"
+                         f"{c['m1']}-{c['m2']}")
+def test_mode_gather_and_scatter_are_the_golden_layout(lib, case):
+    # Integer-valued spectra (every value exact in float32): the gather must pick exactly the
+    # fixture's positions, and the scatter must put each mode back there with zeros everywhere
+    # else, bit for bit.
+    n1, n2, m1, m2 = case["n1"], case["n2"], case["m1"], case["m2"]
+    w = n2 // 2 + 1
+    pos = np.array(case["positions"])
+    batch = 3
+    flat = np.arange(batch * n1 * w, dtype=np.float32)
+    full = (flat + 1j * (flat % 977 - 488)).astype(np.complex64).reshape(batch, n1 * w)
+    fd = torch.from_numpy(full).cuda()
+    md = torch.full((batch, 2 * m1 * m2), 7 + 7j, dtype=torch.complex64, device="cuda")
+    assert lib.spx_gather_modes(_ptr(fd), _ptr(md), n1, w, m1, m2, batch, None) == SPX_OK
+    back = torch.full((batch, n1 * w), 5 - 5j, dtype=torch.complex64, device="cuda")
+    assert lib.spx_scatter_modes(_ptr(md), _ptr(back), n1, w, m1, m2, batch, None) == SPX_OK
+    torch.cuda.synchronize()
+    assert torch.equal(md.cpu(), torch.from_numpy(full[:, pos]))
+    expected = np.zeros_like(full)
+    expected[:, pos] = full[:, pos]
+    assert torch.equal(back.cpu(), torch.from_numpy(expected))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(("n1", "w", "m1", "m2"), [(1, 4096, 0, 33), (1, 7, 0, 7), (4, 3, 0, 2),
+                                                   (4096, 2, 2048, 2), (6, 70, 1, 65)])
+def test_mode_gather_and_scatter_edges(lib, rng, n1, w, m1, m2):
+    # m1 = 0 keeps every row (the 1D pruned layout), every row kept (2 m1 = n1), rows wider than
+    # a wave, and a non-power-of-two n1.
+    batch = 5
+    full = (rng.integers(-99, 99, (batch, n1, w)) + 1j * rng.integers(-99, 99, (batch, n1, w)))
+    full = full.astype(np.complex64)
+    rows = np.r_[0:m1, n1 - m1:n1] if m1 else np.arange(n1)
+    expect_modes = full[:, rows, :m2]
+    fd = torch.from_numpy(full).cuda()
+    md = torch.empty((batch, len(rows), m2), dtype=torch.complex64, device="cuda")
+    assert lib.spx_gather_modes(_ptr(fd), _ptr(md), n1, w, m1, m2, batch, None) == SPX_OK
+    back = torch.full_like(fd, 3 + 3j)
+    assert lib.spx_scatter_modes(_ptr(md), _ptr(back), n1, w, m1, m2, batch, None) == SPX_OK
+    torch.cuda.synchronize()
+    assert torch.equal(md.cpu(), torch.from_numpy(expect_modes))
+    expected = np.zeros_like(full)
+    expected[:, rows, :m2] = expect_modes
+    assert torch.equal(back.cpu(), torch.from_numpy(expected))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(("rows", "cols", "batch"), [(1, 1, 3), (64, 64, 2), (65, 63, 3),
+                                                     (1024, 16384, 1), (3, 200, 7), (513, 1, 2)])
+def test_transpose_is_exact(lib, rng, rows, cols, batch):
+    # Partial tiles on both axes, a single column or row, and the four-step's 1024 x 16384.
+    x = (rng.standard_normal((batch, rows, cols)) + 1j * rng.standard_normal((batch, rows, cols)))
+    xd = torch.from_numpy(x.astype(np.complex64)).cuda()
+    yd = torch.empty(batch, cols, rows, dtype=torch.complex64, device="cuda")
+    assert lib.spx_transpose(_ptr(xd), _ptr(yd), rows, cols, batch, None) == SPX_OK
+    torch.cuda.synchronize()
+    assert torch.equal(yd.cpu(), xd.cpu().transpose(1, 2).contiguous())
+
+
+def _loaded_hip_runtime() -> ctypes.CDLL:
+    # The HIP runtime this process already mapped (the one the library and PyTorch call).
+    for line in Path("/proc/self/maps").read_text().splitlines():
+        path = line.split()[-1]
+        if "libamdhip64.so" in path:
+            return ctypes.CDLL(path)
+    return ctypes.CDLL("libamdhip64.so")
+
+
+@pytest.mark.gpu
+def test_large_transforms_keep_their_workspace_in_the_retained_pool(lib, rng):
+    # A 2^20-point transform takes its scratch from the default pool in stream order; the first
+    # such call raises the pool's release threshold, so after a synchronization the freed scratch
+    # stays reserved for the next call instead of going back to the driver.
+    from oracle import reference as ref
+    from oracle.tolerance import assert_transform_close, random_complex
+
+    n = 1 << 20
+    x = random_complex(rng, (2, n))
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.empty_like(xd)
+    assert lib.spx_c2c(3, _ptr(xd), _ptr(yd), n, 2, 0, None) == SPX_OK, _last(lib)
+    torch.cuda.synchronize()
+    hip = _loaded_hip_runtime()
+    pool = ctypes.c_void_p()
+    assert hip.hipDeviceGetDefaultMemPool(ctypes.byref(pool), torch.cuda.current_device()) == 0
+    threshold = ctypes.c_uint64()
+    assert hip.hipMemPoolGetAttribute(pool, 4, ctypes.byref(threshold)) == 0  # ReleaseThreshold
+    assert threshold.value == 2**64 - 1
+    reserved = ctypes.c_uint64()
+    assert hip.hipMemPoolGetAttribute(pool, 5, ctypes.byref(reserved)) == 0  # ReservedMemCurrent
+    assert reserved.value >= 2 * n * 8
+    assert_transform_close(yd, ref.fft(x), n)

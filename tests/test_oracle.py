@@ -75,6 +75,106 @@ def test_fft2_is_row_transforms_then_column_transforms(rng):
     np.testing.assert_allclose(ref.fft2(x), rows_then_columns, rtol=0, atol=1e-10)
 
 
+def idft_by_sum(modes: np.ndarray, n: int, freqs) -> np.ndarray:
+    """x[m] = (1/n) sum_j modes[j] e^{+2 pi i f_j m / n}, one frequency at a time: the inverse
+    DFT's definition over an explicit list of input frequencies, independent of numpy.fft."""
+    m = np.arange(n)
+    out = np.zeros(modes.shape[:-1] + (n,), dtype=np.complex128)
+    for j, f in enumerate(freqs):
+        out += modes[..., j : j + 1] * np.exp(2j * np.pi * ((f * m) % n) / n)
+    return out / n
+
+
+@pytest.mark.parametrize(("n", "k"), [(1, 1), (8, 1), (8, 3), (16, 16), (64, 17)])
+def test_fft_truncate_is_the_first_outputs_of_the_definition(rng, n, k):
+    x = random_complex(rng, (3, n))
+    np.testing.assert_allclose(ref.fft_truncate(x, k), ref.dft(x)[..., :k], rtol=0,
+                               atol=1e-10 * n)
+    # the last kept bin is frequency k - 1, not k or n - k (a shifted or mirrored slice fails)
+    if 1 < k < n:
+        m = np.arange(n)
+        tone = np.exp(2j * np.pi * (k - 1) * m / n)[None]
+        got = ref.fft_truncate(tone, k)
+        assert np.argmax(np.abs(got[0])) == k - 1 and abs(got[0, k - 1] - n) < 1e-9
+
+
+@pytest.mark.parametrize(("n", "k"), [(1, 1), (8, 1), (8, 3), (32, 32), (64, 17)])
+def test_ifft_from_modes_is_the_inverse_definition_over_the_kept_inputs(rng, n, k):
+    modes = random_complex(rng, (3, k))
+    want = idft_by_sum(modes, n, range(k))
+    np.testing.assert_allclose(ref.ifft_from_modes(modes, n), want, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize(("n", "k0"), [(8, 0), (8, 3), (64, 5), (64, 63)])
+def test_ifft_from_modes_of_a_unit_mode_is_the_closed_form(n, k0):
+    # One unit input at k0: x[m] = e^{+2 pi i k0 m / n} / n (a wrong sign, scale or slot fails).
+    modes = np.zeros((1, k0 + 1), dtype=np.complex128)
+    modes[0, k0] = 1.0
+    m = np.arange(n)
+    np.testing.assert_allclose(ref.ifft_from_modes(modes, n)[0],
+                               np.exp(2j * np.pi * k0 * m / n) / n, rtol=0, atol=1e-15)
+
+
+@pytest.mark.parametrize("n", [1, 8, 64])
+def test_ifft_from_modes_of_every_mode_inverts_fft(rng, n):
+    x = random_complex(rng, (4, n))
+    np.testing.assert_allclose(ref.ifft_from_modes(ref.fft(x), n), x, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize(("n1", "n2"), [(1, 8), (4, 4), (8, 16), (16, 2)])
+def test_ifft2_is_the_inverse_definition(rng, n1, n2):
+    # x[a, b] = (1 / (n1 n2)) sum_{p,q} X[p, q] e^{+2 pi i (p a / n1 + q b / n2)}, evaluated as the
+    # conjugate of the forward definition on both axes.
+    spec = random_complex(rng, (2, n1, n2))
+    rows = ref.dft(np.conj(spec))
+    both = np.swapaxes(ref.dft(np.swapaxes(rows, -1, -2)), -1, -2)
+    np.testing.assert_allclose(ref.ifft2(spec), np.conj(both) / (n1 * n2), rtol=0, atol=1e-12)
+
+
+def test_ifft2_is_column_inverses_of_row_inverses_and_inverts_fft2(rng):
+    x = random_complex(rng, (3, 8, 32))
+    spec = ref.fft2(x)
+    rows_then_columns = np.fft.ifft(ref.ifft(spec), axis=-2)
+    np.testing.assert_allclose(ref.ifft2(spec), rows_then_columns, rtol=0, atol=1e-14)
+    np.testing.assert_allclose(ref.ifft2(spec), x, rtol=0, atol=1e-13)
+    # a separable tone comes back at its own frequency pair with amplitude 1 / (n1 n2)
+    tone = np.zeros((8, 32), dtype=np.complex128)
+    tone[3, 30] = 1.0
+    a, b = np.meshgrid(np.arange(8), np.arange(32), indexing="ij")
+    np.testing.assert_allclose(ref.ifft2(tone), np.exp(2j * np.pi * (3 * a / 8 + 30 * b / 32))
+                               / 256, rtol=0, atol=1e-16)
+
+
+def test_the_pruned_pins_reject_plausible_mistakes(rng):
+    # Mistakes planted in copies of the helpers (on the CPU), each caught by a check above.
+    n, k = 16, 5
+    modes = random_complex(rng, (2, k))
+    want = idft_by_sum(modes, n, range(k))
+
+    def modes_at_the_end(md, nn):  # kept inputs placed at n - k .. n - 1
+        full = np.zeros(md.shape[:-1] + (nn,), dtype=np.complex128)
+        full[..., nn - md.shape[-1]:] = md
+        return np.fft.ifft(full, axis=-1)
+
+    def forward_sign(md, nn):  # e^{-2 pi i k m / n}
+        return np.fft.fft(np.pad(md, [(0, 0), (0, nn - md.shape[-1])]), axis=-1) / nn
+
+    def unscaled(md, nn):  # the 1/n dropped
+        return ref.ifft_from_modes(md, nn) * nn
+
+    for bad in (modes_at_the_end, forward_sign, unscaled):
+        assert not np.allclose(bad(modes, n), want, rtol=0, atol=1e-6), bad.__name__
+    x = random_complex(rng, (2, n))
+    assert not np.allclose(ref.fft(x)[..., 1 : k + 1], ref.dft(x)[..., :k], atol=1e-6)
+    spec = random_complex(rng, (8, 16))
+    rows = ref.dft(np.conj(spec))
+    defn = np.conj(np.swapaxes(ref.dft(np.swapaxes(rows, -1, -2)), -1, -2)) / 128
+    for bad in (np.fft.ifft(spec, axis=-1),  # rows only
+                np.fft.fft2(spec) / 128,  # forward sign
+                np.fft.ifft2(spec) * 128):  # unscaled
+        assert not np.allclose(bad, defn, rtol=0, atol=1e-6)
+
+
 def test_rfft2_truncate_keeps_the_lowest_modes(rng):
     # The reference's known answer (test_reference.py:53-59), restated.
     x = random_real(rng, (2, 16, 16))

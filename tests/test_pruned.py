@@ -1,7 +1,8 @@
 """Pruned transforms against the float64 oracle, every implementation (reference
 tests/test_pruned.py): the Stockham kernels prune inside the kernel, naive gathers from (or
-scatters into) a full transform. The mode layout is checked bit-exactly where the arithmetic is
-exact."""
+scatters into) a full transform. The mode layout is checked bit for bit: through the transforms
+on integer-valued modes (rounded after the transform), and through the C ABI's gather and scatter
+in tests/test_capi.py."""
 
 import json
 from pathlib import Path
@@ -83,39 +84,44 @@ def test_irfft2_from_modes_matches_the_oracle(rng, impl, n1, n2, m1, m2):
     assert_transform_close(y, ref.irfft2_from_modes(modes, (n1, n2)), n1 * n2, axes=AXES)
 
 
-@pytest.mark.parametrize("impl", IMPLS)
-def test_mode_layout_is_bit_exact_on_single_modes(impl):
-    # One unit mode at a time through irfft2_from_modes and back: each kept position must come
-    # back at exactly its own index (the layout of tests/golden/modes_index.json), with every
-    # other mode at rounding level.
-    n1, n2, m1, m2 = 16, 16, 3, 4
-    rows = 2 * m1
-    eye = np.zeros((rows * m2, rows, m2), dtype=np.complex64)
-    for e in range(rows * m2):
-        eye[e].flat[e] = 1.0
-    fields = spectral.irfft2_from_modes(cuda(eye), (n1, n2), impl=impl)
-    back = spectral.rfft2_truncated(fields, m1, m2, impl=impl).cpu().numpy()
-    peak = np.abs(back).reshape(rows * m2, -1).argmax(axis=1)
-    # column-0 modes fold with their conjugate partner in a real field, so only c > 0 is exact
-    for e in range(rows * m2):
-        r, c = divmod(e, m2)
-        if c != 0:
-            assert peak[e] == e, (e, peak[e])
-
-
-def test_mode_layout_matches_the_golden_fixture():
+def golden_positions(n1: int, n2: int, m1: int, m2: int) -> np.ndarray:
     data = json.loads((Path(__file__).parent / "golden" / "modes_index.json").read_text())
-    case = next(c for c in data if (c["n1"], c["n2"], c["m1"], c["m2"]) == (128, 128, 16, 16))
-    # A field whose full half spectrum holds its own flat index: exact in float32 below 2^24.
-    n1, n2, m1, m2 = case["n1"], case["n2"], case["m1"], case["m2"]
+    case = next(c for c in data if (c["n1"], c["n2"], c["m1"], c["m2"]) == (n1, n2, m1, m2))
+    return np.array(case["positions"])
+
+
+# Golden-fixture shapes with at least one column between DC and Nyquist.
+LAYOUT_CASES = [(8, 8, 2, 3), (16, 16, 3, 4), (16, 16, 8, 9), (64, 32, 12, 12), (32, 128, 4, 20),
+                (128, 128, 16, 16)]
+
+
+@pytest.mark.parametrize("impl", IMPLS)
+@pytest.mark.parametrize(("n1", "n2", "m1", "m2"), LAYOUT_CASES)
+def test_mode_layout_is_exact_through_the_transforms(impl, n1, n2, m1, m2):
+    # Distinct integers placed at the fixture's positions of a half spectrum (columns 0 and n2/2,
+    # where a real field ties a mode to its conjugate partner, left zero), turned into a real
+    # field on the CPU. The GPU forward must return every integer in its own slot of the mode
+    # block: its float32 error is far below 0.5 at these sizes, so rounding to the nearest
+    # integer compares the layout bit for bit. The GPU inverse of the integer block, taken back
+    # through the float64 forward and rounded, must be the same half spectrum, zeros included.
     w = n2 // 2 + 1
-    for impl in IMPLS:
-        rng = np.random.default_rng(7)
-        x = rng.standard_normal((2, n1, n2)).astype(np.float32)
-        full = spectral.rfft2(cuda(x), impl=impl).cpu().numpy().reshape(2, -1)
-        modes = spectral.rfft2_truncated(cuda(x), m1, m2, impl=impl).cpu().numpy().reshape(2, -1)
-        assert_transform_close(modes, full[:, case["positions"]], n1 * n2, axes=(-1,))
-        assert full.shape[1] == n1 * w
+    pos = golden_positions(n1, n2, m1, m2)
+    free = (pos % w != 0) & (pos % w != n2 // 2)
+    count = int(free.sum())
+    ids = np.zeros((2, pos.size), dtype=np.complex128)
+    ids[:, free] = (np.arange(1, 2 * count + 1) - 1j * np.arange(2 * count, 0, -1)).reshape(2, -1)
+    full = np.zeros((2, n1 * w), dtype=np.complex128)
+    full[:, pos] = ids
+    field = ref.irfft2(full.reshape(2, n1, w), (n1, n2)).astype(np.float32)
+
+    modes = spectral.rfft2_truncated(cuda(field), m1, m2, impl=impl).cpu().numpy()
+    got = modes.reshape(2, -1).astype(np.complex128)
+    assert np.array_equal(np.round(got.real) + 1j * np.round(got.imag), ids)
+
+    block = cuda(ids.reshape(2, 2 * m1, m2).astype(np.complex64))
+    back = spectral.irfft2_from_modes(block, (n1, n2), impl=impl).cpu().numpy()
+    spec = ref.rfft2(back).reshape(2, -1)
+    assert np.array_equal(np.round(spec.real) + 1j * np.round(spec.imag), full)
 
 
 @pytest.mark.parametrize("impl", IMPLS)
