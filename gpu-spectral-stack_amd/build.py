@@ -60,6 +60,7 @@ CAPI_SOURCES = [
     "naive.hip",
     "scale.hip",
     "remap.hip",
+    "noalloc.hip",
     "fft2d.hip",
     "pruned.hip",
     "ns.hip",

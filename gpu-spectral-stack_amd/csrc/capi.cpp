@@ -157,6 +157,15 @@ int spx_c2c(int impl, const void* x, void* y, int n, int batch, int inverse, hip
     return guarded([&] { impl_at(impl).c2c(cc(x), cm(y), n, batch, dir(inverse), stream); });
 }
 
+int spx_c2c_noalloc(int impl, const void* x, void* y, int n, int batch, int inverse,
+                    hipStream_t stream)
+{
+    static_assert(SPX_NOALLOC_SCRATCH_VALUES == spx::kNoAllocScratchValues,
+                  "the header's scratch size must match the library's");
+    return guarded(
+        [&] { spx::c2c_noalloc(impl_at(impl), cc(x), cm(y), n, batch, dir(inverse), stream); });
+}
+
 int spx_r2c(int impl, const float* x, void* y, int n, int batch, void* work, hipStream_t stream)
 {
     return guarded([&] { impl_at(impl).r2c(x, cm(y), n, batch, cm(work), stream); });

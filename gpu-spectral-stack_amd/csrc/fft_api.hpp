@@ -29,6 +29,8 @@ using C2rFn = void (*)(const cf32* x, float* y, int n, int batch, cf32* work,
                        hipStream_t stream);
 using ColumnsFn = void (*)(const cf32* x, cf32* y, int n, int cols, int slabs,
                            Direction direction, hipStream_t stream);
+using C2cWorkFn = void (*)(const cf32* x, cf32* y, int n, int batch, Direction direction,
+                           cf32* work, hipStream_t stream);
 
 // reference fft.hpp:62-72
 struct PrunedFns {
@@ -102,7 +104,21 @@ struct FftImpl {
     bool real_needs_work;     // r2c and c2r use the work buffer
     const Fused2dFns* fused;  // single-pass 2D kernels, or nullptr
     const RfFns* rf;          // the radio callers' fused kernels, or nullptr
+    // c2c with the caller's scratch for the sizes that need one (c2c_scratch_values), instead
+    // of scratch allocated on the stream; nullptr when no size needs scratch.
+    C2cWorkFn c2c_work;
 };
+
+// Scratch values c2c_work needs for batch transforms of n points: n x batch beyond the
+// single-pass sizes (the two-pass and four-step intermediates), none up to kSinglePassMaxN.
+std::size_t c2c_scratch_values(const FftImpl& impl, int n, int batch);
+
+// c2c that allocates nothing (noalloc.hip): large transforms use a static per-device scratch of
+// kNoAllocScratchValues values. Throws InvalidArgument past that, or for an implementation whose
+// first call allocates a table.
+constexpr std::size_t kNoAllocScratchValues = std::size_t(1) << 22;  // 32 MiB of cf32
+void c2c_noalloc(const FftImpl& impl, const cf32* x, cf32* y, int n, int batch,
+                 Direction direction, hipStream_t stream);
 
 // The registry, in the reference's order (registry.hpp:28-40).
 const FftImpl* impls();
@@ -213,6 +229,8 @@ void ns_stage(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf
 #define SPX_DECLARE_VARIANT(NAME)                                                               \
     void c2c_##NAME(const cf32* x, cf32* y, int n, int batch, Direction direction,             \
                     hipStream_t stream);                                                        \
+    void c2c_work_##NAME(const cf32* x, cf32* y, int n, int batch, Direction direction,        \
+                         cf32* work, hipStream_t stream);                                       \
     void r2c_##NAME(const float* x, cf32* y, int n, int batch, cf32* work, hipStream_t stream); \
     void c2r_##NAME(const cf32* x, float* y, int n, int batch, cf32* work, hipStream_t stream); \
     void columns_##NAME(const cf32* x, cf32* y, int n, int cols, int slabs,                    \

@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <atomic>
 #include <climits>
+#include <optional>
 #include <type_traits>
 
 namespace spx {
@@ -444,6 +445,24 @@ private:
     bool pooled_;
 };
 
+// The scratch of one large-transform call: `given` when the caller brings it (at least
+// n x batch values), otherwise a StreamWorkspace of that size.
+class CallScratch {
+public:
+    CallScratch(cf32* given, std::size_t count, hipStream_t stream) : ptr_(given)
+    {
+        if (ptr_ == nullptr) {
+            own_.emplace(count, stream);
+            ptr_ = own_->get();
+        }
+    }
+    cf32* get() const { return ptr_; }
+
+private:
+    cf32* ptr_;
+    std::optional<StreamWorkspace> own_;
+};
+
 template <int R, bool Table>
 struct Stockham {
     // Complex transforms of n <= 4096 points. keep prunes the frequency side: forward writes the
@@ -486,7 +505,7 @@ struct Stockham {
     // the n2 columns of each n1 x n2 matrix (x -> work), then the twiddled n2-point rows, stored
     // transposed (work -> y): X[k1 + n1 k2] is row k1's element k2.
     static void two_pass(const cf32* x, cf32* y, int n, int batch, Direction direction,
-                         hipStream_t stream)
+                         hipStream_t stream, cf32* given)
     {
         const int n2 = n <= (1 << 18) ? 512 : 1024;
         const int n1 = n / n2;
@@ -496,7 +515,7 @@ struct Stockham {
         }
         const bool inverse = direction == Direction::Inverse;
         const std::size_t total = static_cast<std::size_t>(n) * static_cast<std::size_t>(batch);
-        StreamWorkspace work(total, stream);
+        const CallScratch work(given, total, stream);
         columns_impl(x, work.get(), n1, n2, batch, direction, stream, 0, 0, false);
         const dev::TwiddleRowsTransposedIo rows{
             dev::TwiddleRowsIo{work.get(), y, inverse ? 1.0f / static_cast<float>(n2) : 1.0f,
@@ -524,8 +543,9 @@ struct Stockham {
 
     // Any power of two up to kFourStepMaxN: one kernel up to kSinglePassMaxN, two passes up to
     // kTwoPassMaxN, four steps beyond.
+    // work: nullptr, or the caller's scratch of c2c_scratch_values(n, batch) values.
     static void c2c(const cf32* x, cf32* y, int n, int batch, Direction direction,
-                    hipStream_t stream)
+                    hipStream_t stream, cf32* work = nullptr)
     {
         if (n <= kStockhamMaxN) {
             c2c_single(x, y, n, batch, direction, stream, n);
@@ -553,7 +573,7 @@ struct Stockham {
             return;
         }
         if (n <= kTwoPassMaxN) {
-            two_pass(x, y, n, batch, direction, stream);
+            two_pass(x, y, n, batch, direction, stream, work);
             return;
         }
         // Rows of kSinglePassMaxN points (one kernel each), so the columns are short (n1 <= 1024
@@ -565,12 +585,12 @@ struct Stockham {
             throw InvalidArgument("fourstep: too many transforms");
         }
         const bool inverse = direction == Direction::Inverse;
-        StreamWorkspace work(total, stream);
+        const CallScratch scratch(work, total, stream);
         // 1. n1-point transforms down the n2 columns of each n1 x n2 matrix (x -> y).
         columns_impl(x, y, n1, n2, batch, direction, stream, 0, 0, false);
-        // 2 + 3. Twiddle, then n2-point rows (y -> work).
+        // 2 + 3. Twiddle, then n2-point rows (y -> scratch).
         const dev::TwiddleRowsIo rows{y,
-                                      work.get(),
+                                      scratch.get(),
                                       inverse ? 1.0f / static_cast<float>(n2) : 1.0f,
                                       inverse ? 1.0f : -1.0f,
                                       n1,
@@ -582,8 +602,8 @@ struct Stockham {
             dev::dispatch_large<R, false, Table>(n2, rows, static_cast<long long>(batch) * n1,
                                                  stream);
         }
-        // 4. Row k1, column k2 holds X[k1 + n1 k2]: transpose each matrix (work -> y).
-        transpose(work.get(), y, n1, n2, batch, stream);
+        // 4. Row k1, column k2 holds X[k1 + n1 k2]: transpose each matrix (scratch -> y).
+        transpose(scratch.get(), y, n1, n2, batch, stream);
     }
 
     // Columns of n = 2048 or 4096 points as two passes of 64 x (n / 64) (four-step on the column
@@ -1174,6 +1194,11 @@ struct RfDriver {
                     hipStream_t stream)                                                         \
     {                                                                                           \
         Stockham<R, TABLE>::c2c(x, y, n, batch, direction, stream);                             \
+    }                                                                                           \
+    void c2c_work_##NAME(const cf32* x, cf32* y, int n, int batch, Direction direction,        \
+                         cf32* work, hipStream_t stream)                                        \
+    {                                                                                           \
+        Stockham<R, TABLE>::c2c(x, y, n, batch, direction, stream, work);                       \
     }                                                                                           \
     void r2c_##NAME(const float* x, cf32* y, int n, int batch, cf32* work, hipStream_t stream) \
     {                                                                                           \

@@ -76,6 +76,19 @@ int spx_scale(const void* x, void* y, size_t n, float alpha, hipStream_t stream)
  * columns: slabs row-major arrays of n rows by cols columns; transforms every column, in place
  *      when x == y. Only implementations with has_columns. */
 int spx_c2c(int impl, const void* x, void* y, int n, int batch, int inverse, hipStream_t stream);
+
+/* --- c2c without allocation: no counterpart in the reference ----------------------------------
+ * For callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, kernels and results as spx_c2c, but
+ * the scratch of the large transforms (n > 16384: n * batch complex values) lives in a static
+ * per-device array of SPX_NOALLOC_SCRATCH_VALUES complex values (32 MiB, held by every GPU the
+ * library runs on until the process ends), and the call makes no hipMalloc, hipMallocAsync or
+ * hipFree. Returns SPX_EINVAL when n * batch exceeds that array (n > 16384), and for
+ * stockham_r8_table (its twiddle table is allocated on first use). Calls that overlap on one GPU
+ * race on the shared array. */
+#define SPX_NOALLOC_SCRATCH_VALUES (1u << 22)
+int spx_c2c_noalloc(int impl, const void* x, void* y, int n, int batch, int inverse,
+                    hipStream_t stream);
 int spx_r2c(int impl, const float* x, void* y, int n, int batch, void* work, hipStream_t stream);
 int spx_c2r(int impl, const void* x, float* y, int n, int batch, void* work, hipStream_t stream);
 int spx_columns(int impl, const void* x, void* y, int n, int cols, int slabs, int inverse,

@@ -443,3 +443,18 @@ def test_large_transforms_keep_their_workspace_in_the_retained_pool(lib, rng):
     assert hip.hipMemPoolGetAttribute(pool, 5, ctypes.byref(reserved)) == 0  # ReservedMemCurrent
     assert reserved.value >= 2 * n * 8
     assert_transform_close(yd, ref.fft(x), n)
+
+
+def test_noalloc_c2c_rejects_what_its_static_scratch_cannot_hold(lib):
+    # Checked on the host before anything is queued: more than 2^22 values of scratch, and the
+    # table variant (whose first call allocates its table).
+    p = ctypes.c_void_p(0x1000)
+    q = ctypes.c_void_p(0x10000000)
+    assert lib.spx_c2c_noalloc(3, p, q, 1 << 20, 5, 0, None) == SPX_EINVAL
+    assert "split the batch" in _last(lib)
+    assert lib.spx_c2c_noalloc(3, p, q, 1 << 24, 1, 0, None) == SPX_EINVAL
+    assert lib.spx_c2c_noalloc(4, p, q, 1 << 20, 1, 0, None) == SPX_EINVAL
+    assert "twiddle table" in _last(lib)
+    assert lib.spx_c2c_noalloc(3, p, q, 3 << 20, 1, 0, None) == SPX_EINVAL
+    assert "power of two" in _last(lib)
+    assert lib.spx_c2c_noalloc(3, p, q, 1 << 20, 0, 0, None) == SPX_EINVAL
