@@ -252,6 +252,7 @@ def main(argv=None) -> int:
     if not args.no_extra:
         extra.update(secondary_rows(args.impl, dev))
         extra.update(capi_rows(lib, impl, dev, stream))
+        extra.update(sweep_rows(lib, impl, dev, stream))
         extra.update(navier_stokes_rows(args.impl, dev))
         extra.update(radio_rows(args.impl, dev))
 
@@ -366,6 +367,88 @@ def secondary_rows(impl: str, dev) -> dict:
     xc = [torch.randn(BATCH, N, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
     out["c1_rocfft_c2c_1024_fwd_ms"] = round(timed(torch.fft.fft, xc), 5)
     return out
+
+
+def sweep_rows(lib, impl: int, dev, stream) -> dict:
+    """BASELINE C2's sweep and C1's sizes: C2C, R2C and C2R at n = 2, 4, ..., 4096 with
+    batch = 2^24 / n, through the C ABI on `stream`, next to rocFFT (torch.fft) on the same shapes.
+    Three buffer sets of 2^24 complex values each (384 MiB per side, 768 MiB in rotation) serve
+    every size. Rows [n, us, % of 8 TB/s, rocFFT us, rocFFT %] per op, times the median of 5
+    rounds of 20 launches after 3 warm-ups; bytes follow the reference's convention
+    (16 B per C2C point, 4n + 8(n/2 + 1) B per real row)."""
+    import statistics
+
+    import torch
+
+    from spectral.benchmark import fft_c2c_work, fft_real_work, time_gpu
+
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    g = torch.Generator(device=dev).manual_seed(2)
+    total = 1 << 24
+    ins = [torch.randn(total, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
+    outs = [torch.empty(total, dtype=torch.complex64, device=dev) for _ in range(3)]
+    torch.cuda.synchronize()
+    vp = ctypes.c_void_p
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(lib.spx_last_error().decode())
+
+    def median_us(call):
+        for i in range(3):
+            call(i % 3)
+        runs = []
+        for _ in range(5):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for i in range(20):
+                call(i % 3)
+            b.record(stream)
+            b.synchronize()
+            runs.append(a.elapsed_time(b) / 20 * 1e3)
+        return statistics.median(runs)
+
+    def torch_us(fn, inputs):
+        k = [0]
+
+        def call():
+            k[0] += 1
+            return fn(inputs[k[0] % 3])
+
+        return time_gpu(call).median_ms * 1e3
+
+    rows = {"c2c": [], "r2c": [], "c2r": []}
+    n = 2
+    while n <= 4096:
+        batch = total // n
+        half = n // 2 + 1
+        c2c_bytes = fft_c2c_work(n, batch)[1]
+        real_bytes = fft_real_work(n, batch)[1]
+        as_c = [x.view(batch, n) for x in ins]
+        as_r = [x.view(torch.float32)[:total].view(batch, n) for x in ins]
+        as_h = [x[: batch * half].view(batch, half) for x in ins]
+        for op, nbytes, ours, theirs, inputs in (
+            ("c2c", c2c_bytes,
+             lambda i: check(lib.spx_c2c(impl, vp(ins[i].data_ptr()), vp(outs[i].data_ptr()), n,
+                                         batch, 0, sptr)),
+             torch.fft.fft, as_c),
+            ("r2c", real_bytes,
+             lambda i: check(lib.spx_r2c(impl, vp(ins[i].data_ptr()), vp(outs[i].data_ptr()), n,
+                                         batch, None, sptr)),
+             torch.fft.rfft, as_r),
+            ("c2r", real_bytes,
+             lambda i: check(lib.spx_c2r(impl, vp(ins[i].data_ptr()), vp(outs[i].data_ptr()), n,
+                                         batch, None, sptr)),
+             lambda h: torch.fft.irfft(h, n), as_h),
+        ):
+            us = median_us(ours)
+            roc = torch_us(theirs, inputs)
+            rows[op].append([n, round(us, 2), round(100 * nbytes / (us * 1e3) / PEAK_GBPS, 1),
+                             round(roc, 2), round(100 * nbytes / (roc * 1e3) / PEAK_GBPS, 1)])
+        n *= 2
+    del ins, outs
+    return {"c2_sweep": rows}
 
 
 def capi_rows(lib, impl: int, dev, stream) -> dict:

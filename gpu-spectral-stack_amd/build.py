@@ -6,9 +6,11 @@
    hipcc for --offload-arch=gfx950 only; depends on the HIP runtime and nothing from PyTorch.
 2. spectral/_C.so: the PyTorch operators (TORCH_LIBRARY "spectral") over that C ABI. Plain
    C++ against the PyTorch-ROCm headers, linked to libspectral_hip.so through $ORIGIN.
-3. bin/spectral_peaks: the measured copy-bandwidth and FP32 ceilings (csrc/tools/peaks.hip), and
+3. bin/spectral_peaks: the measured copy-bandwidth and FP32 ceilings (csrc/tools/peaks.hip),
    bin/spectral_bench: every implementation of every operation next to rocFFT, as CSV
-   (csrc/tools/spectral_bench.cpp, over the C ABI of libspectral_hip.so).
+   (csrc/tools/spectral_bench.cpp, over the C ABI of libspectral_hip.so), and
+   bin/spectral_mfma_dft: C4's pruned column pass as FFTs and as an fp32 matrix-core DFT
+   (csrc/tools/mfma_dft.hip).
 
 Both land in python/spectral/, next to the Python package that loads them. Object files go to
 _build/ (git-ignored). Every call recompiles what is older than its sources.
@@ -79,6 +81,8 @@ TOOLS = {
     "spectral_bench": (CSRC / "tools" / "spectral_bench.cpp",
                        ["-x", "hip", f"-L{PKG}", "-lspectral_hip", "-lhipfft",
                         "-Wl,-rpath,$ORIGIN/../python/spectral"]),
+    "spectral_mfma_dft": (CSRC / "tools" / "mfma_dft.hip",
+                          [f"-L{PKG}", "-lspectral_hip", "-Wl,-rpath,$ORIGIN/../python/spectral"]),
 }
 
 
