@@ -250,9 +250,9 @@ def main(argv=None) -> int:
     extra["copy_gbps"] = round(copy_gbps, 1)
     extra["c1_pct_of_copy"] = round(100 * value / copy_gbps, 1)
     if not args.no_extra:
+        extra.update(sweep_rows(lib, impl, dev, stream))
         extra.update(secondary_rows(args.impl, dev))
         extra.update(capi_rows(lib, impl, dev, stream))
-        extra.update(sweep_rows(lib, impl, dev, stream))
         extra.update(navier_stokes_rows(args.impl, dev))
         extra.update(radio_rows(args.impl, dev))
 
@@ -373,14 +373,17 @@ def sweep_rows(lib, impl: int, dev, stream) -> dict:
     """BASELINE C2's sweep and C1's sizes: C2C, R2C and C2R at n = 2, 4, ..., 4096 with
     batch = 2^24 / n, through the C ABI on `stream`, next to rocFFT (torch.fft) on the same shapes.
     Three buffer sets of 2^24 complex values each (384 MiB per side, 768 MiB in rotation) serve
-    every size. Rows [n, us, % of 8 TB/s, rocFFT us, rocFFT %] per op, times the median of 5
-    rounds of 20 launches after 3 warm-ups; bytes follow the reference's convention
-    (16 B per C2C point, 4n + 8(n/2 + 1) B per real row)."""
+    every size. The sizes are interleaved: each of 9 rounds times 20 launches of every (op, n),
+    after 2 untimed ones, so a transient slowdown of the device lands in a round or two of each
+    row instead of all of one row's; a row reports the median round. This stack's rows are all
+    timed before rocFFT's. Rows are
+    [n, us, % of 8 TB/s, rocFFT us, rocFFT %]; bytes follow the reference's convention (16 B per
+    C2C point, 4n + 8(n/2 + 1) B per real row)."""
     import statistics
 
     import torch
 
-    from spectral.benchmark import fft_c2c_work, fft_real_work, time_gpu
+    from spectral.benchmark import fft_c2c_work, fft_real_work
 
     sptr = ctypes.c_void_p(stream.cuda_stream)
     g = torch.Generator(device=dev).manual_seed(2)
@@ -394,61 +397,64 @@ def sweep_rows(lib, impl: int, dev, stream) -> dict:
         if rc != 0:
             raise RuntimeError(lib.spx_last_error().decode())
 
-    def median_us(call):
-        for i in range(3):
-            call(i % 3)
-        runs = []
-        for _ in range(5):
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for i in range(20):
-                call(i % 3)
-            b.record(stream)
-            b.synchronize()
-            runs.append(a.elapsed_time(b) / 20 * 1e3)
-        return statistics.median(runs)
-
-    def torch_us(fn, inputs):
-        k = [0]
-
-        def call():
-            k[0] += 1
-            return fn(inputs[k[0] % 3])
-
-        return time_gpu(call).median_ms * 1e3
-
-    rows = {"c2c": [], "r2c": [], "c2r": []}
+    rows = []  # (op, n, bytes, ours(i), theirs(i), [our us], [rocFFT us])
     n = 2
     while n <= 4096:
         batch = total // n
         half = n // 2 + 1
-        c2c_bytes = fft_c2c_work(n, batch)[1]
-        real_bytes = fft_real_work(n, batch)[1]
         as_c = [x.view(batch, n) for x in ins]
         as_r = [x.view(torch.float32)[:total].view(batch, n) for x in ins]
         as_h = [x[: batch * half].view(batch, half) for x in ins]
-        for op, nbytes, ours, theirs, inputs in (
-            ("c2c", c2c_bytes,
-             lambda i: check(lib.spx_c2c(impl, vp(ins[i].data_ptr()), vp(outs[i].data_ptr()), n,
-                                         batch, 0, sptr)),
-             torch.fft.fft, as_c),
-            ("r2c", real_bytes,
-             lambda i: check(lib.spx_r2c(impl, vp(ins[i].data_ptr()), vp(outs[i].data_ptr()), n,
-                                         batch, None, sptr)),
-             torch.fft.rfft, as_r),
-            ("c2r", real_bytes,
-             lambda i: check(lib.spx_c2r(impl, vp(ins[i].data_ptr()), vp(outs[i].data_ptr()), n,
-                                         batch, None, sptr)),
-             lambda h: torch.fft.irfft(h, n), as_h),
-        ):
-            us = median_us(ours)
-            roc = torch_us(theirs, inputs)
-            rows[op].append([n, round(us, 2), round(100 * nbytes / (us * 1e3) / PEAK_GBPS, 1),
-                             round(roc, 2), round(100 * nbytes / (roc * 1e3) / PEAK_GBPS, 1)])
+
+        def c2c(i, n=n, batch=batch):
+            check(lib.spx_c2c(impl, vp(ins[i].data_ptr()), vp(outs[i].data_ptr()), n, batch, 0,
+                              sptr))
+
+        def r2c(i, n=n, batch=batch):
+            check(lib.spx_r2c(impl, vp(ins[i].data_ptr()), vp(outs[i].data_ptr()), n, batch,
+                              None, sptr))
+
+        def c2r(i, n=n, batch=batch):
+            check(lib.spx_c2r(impl, vp(ins[i].data_ptr()), vp(outs[i].data_ptr()), n, batch,
+                              None, sptr))
+
+        rows.append(("c2c", n, fft_c2c_work(n, batch)[1], c2c,
+                     lambda i, a=as_c: torch.fft.fft(a[i]), [], []))
+        rows.append(("r2c", n, fft_real_work(n, batch)[1], r2c,
+                     lambda i, a=as_r: torch.fft.rfft(a[i]), [], []))
+        rows.append(("c2r", n, fft_real_work(n, batch)[1], c2r,
+                     lambda i, a=as_h, n=n: torch.fft.irfft(a[i], n), [], []))
         n *= 2
-    del ins, outs
-    return {"c2_sweep": rows}
+
+    def timed_us(run, on):
+        for i in range(2):
+            run(i)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(on)
+        for i in range(20):
+            run(i % 3)
+        b.record(on)
+        b.synchronize()
+        return a.elapsed_time(b) / 20 * 1e3
+
+    # Ours over every row first, then rocFFT's: rocFFT's kernels on random data, timed between
+    # ours, slowed the following launches of this stack's 1024- to 4096-point C2C by 5-12 %
+    # (the same launches after rocFFT on zeros, or alone, were not slowed).
+    current = torch.cuda.current_stream(dev)
+    for _ in range(9):
+        for _, _, _, ours, _, us, _ in rows:
+            us.append(timed_us(ours, stream))
+    for _ in range(9):
+        for _, _, _, _, theirs, _, roc in rows:
+            roc.append(timed_us(theirs, current))
+    out = {"c2c": [], "r2c": [], "c2r": []}
+    for op, n, nbytes, _, _, us, roc in rows:
+        t, r = statistics.median(us), statistics.median(roc)
+        out[op].append([n, round(t, 2), round(100 * nbytes / (t * 1e3) / PEAK_GBPS, 1),
+                        round(r, 2), round(100 * nbytes / (r * 1e3) / PEAK_GBPS, 1)])
+    del ins, outs, rows
+    return {"c2_sweep": out}
 
 
 def capi_rows(lib, impl: int, dev, stream) -> dict:

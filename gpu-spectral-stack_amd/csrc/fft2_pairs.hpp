@@ -162,22 +162,25 @@ struct PairR2cIo {
     {
         if constexpr (direct_combine<P>()) {
             // X[0 .. N] of each row, combined by final: consecutive lanes take consecutive
-            // values of a row, so every store instruction writes long contiguous runs. (Storing
-            // straight from final's registers, runs of L values into rows that start at 8-byte
-            // offsets, measured 5.0 points of the peak slower at 256^2 and 1.8 at 512^2.)
+            // values of a row, each row walked in whole 128-byte lines from the boundary before
+            // its start (its N + 1 values start at an 8-byte offset; stores straddling lines
+            // wrote 7 % more bytes than the output holds at 512^2). (Storing straight from
+            // final's registers, runs of L values, measured 5.0 points of the peak slower at
+            // 256^2 and 1.8 at 512^2 than the row-walk store before this one.)
             constexpr int N = P::N;
-            using S = Staged<G, N + 1>;
             const long long array0 = (first >> 1) / rows.pairs;
             const int k10 = static_cast<int>((first >> 1) - array0 * rows.pairs);
-            S::each(count, tid, [&](int, int u, int k, bool valid) {
-                long long array;
-                bool dup;
-                const int r = rows.row_after(array0, k10, u, array, dup);
-                if (valid && !dup) {
-                    st_stream(y + (array * rows.n1 + r) * (N + 1) + k,
-                              lds[u * P::kStride + pad(k)]);
-                }
-            });
+            cf32* const out = y;
+            const PairRows pr = rows;
+            store_rows_aligned<G, N + 1, P::kStride>(
+                lds, count, tid,
+                [&](int u) -> cf32* {
+                    long long array;
+                    bool dup;
+                    const int r = pr.row_after(array0, k10, u, array, dup);
+                    return dup ? nullptr : out + (array * pr.n1 + r) * (N + 1);
+                },
+                [](cf32* p, cf32 v) { st_stream(p, v); });
             return;
         }
         constexpr int N = P::N;

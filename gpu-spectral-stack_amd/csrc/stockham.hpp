@@ -37,6 +37,7 @@
 
 #include "spx_common.hpp"
 
+#include <cstdint>
 #include <type_traits>
 
 namespace spx::dev {
@@ -640,6 +641,58 @@ struct Staged {
     }
 };
 
+// The group's rows of Row values written out as one run: row u of LDS (lds + u * Stride, value
+// i at pad(i)) to dst[u * Row + i] for u < count. Consecutive lanes take consecutive values of
+// the run, walked from the 128-byte boundary at or before dst, so every wave store covers whole
+// lines whatever the row length: rows of odd length (a half spectrum's m + 1 values) start at
+// 8-byte offsets, and a store straddling lines leaves partial lines that nontemporal writes
+// send to memory separately. put(address, value) does the store.
+template <class G, int Row, int Stride, class Put>
+__device__ __forceinline__ void store_run_aligned(const cf32* lds, cf32* dst, int count, int tid,
+                                                  Put&& put)
+{
+    constexpr int kTotal = G::kT * Row;
+    constexpr int kSteps = (kTotal + 15 + G::kThreads - 1) / G::kThreads;
+    const int shift = static_cast<int>((reinterpret_cast<std::uintptr_t>(dst) / sizeof(cf32)) & 15);
+    const int total = (G::kFull ? G::kT : count) * Row;
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+        const int e = tid + k * G::kThreads - shift;
+        if (e >= 0 && e < total) {
+            const int u = e / Row;
+            const int i = e - u * Row;
+            put(dst + e, lds[u * Stride + pad(i)]);
+        }
+    }
+}
+
+// The same for rows that are not adjacent in memory: row u of LDS to dst(u)[0 .. Row), or
+// nowhere when dst(u) is null. Each row is walked over a span of whole 128-byte lines from the
+// boundary at or before its start (Span slots, enough for any start), consecutive lanes on
+// consecutive slots.
+template <class G, int Row, int Stride, class Dst, class Put>
+__device__ __forceinline__ void store_rows_aligned(const cf32* lds, int count, int tid, Dst&& dst,
+                                                   Put&& put)
+{
+    constexpr int kSpan = (Row + 15 + 15) / 16 * 16;
+    constexpr int kSteps = (G::kT * kSpan + G::kThreads - 1) / G::kThreads;
+    const int rows = G::kFull ? G::kT : count;
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+        const int e = tid + k * G::kThreads;
+        const int u = e / kSpan;
+        cf32* const d = u < rows ? dst(u) : nullptr;
+        if (d != nullptr) {
+            const int shift = static_cast<int>((reinterpret_cast<std::uintptr_t>(d) / sizeof(cf32))
+                                               & 15);
+            const int i = e - u * kSpan - shift;
+            if (i >= 0 && i < Row) {
+                put(d + i, lds[u * Stride + pad(i)]);
+            }
+        }
+    }
+}
+
 // --- the kernel -----------------------------------------------------------------------------
 //
 // An I/O policy `Io` supplies, for transform t of the batch:
@@ -841,7 +894,7 @@ struct C2cIo {
 // so one twiddle serves bins k and m-k (k = 0 pairs with m, whose Z index wraps to 0). This is the
 // split formula of the reference's real.cuh:7-42, evaluated per pair instead of per bin.
 // keep: values per row of y, m + 1 for the whole half spectrum, fewer when pruned.
-template <bool PlainOut>
+template <bool PlainOut, bool Aligned = true>
 struct R2cIoT {
     static constexpr bool kGroupIsBlock = false;
     static constexpr bool kFinal = true;
@@ -849,12 +902,23 @@ struct R2cIoT {
     cf32* y;
     int keep;
 
-    // Rows of 64 lanes or more (m >= 512 at radix 8) store their bins X[k] straight from
-    // registers, each store a run of L values, with no staged store behind. Rows of m + 1 values
-    // start at 8-byte offsets: shorter runs, from 16 or 32 lanes, measured 7-23 points slower
-    // than the staged store's contiguous run per workgroup.
+    // The group's rows leave LDS as one run in whole 128-byte lines (store_run_aligned): rows of
+    // m + 1 values start at 8-byte offsets, and stores that straddle lines wrote 5-9 % more bytes
+    // than the output holds (WRITE_SIZE, n = 128 .. 8192); in whole lines, 0.2-1.8 %. Rows of
+    // fewer than 64 lanes are staged through LDS anyway. Rows of 64 lanes or more take it when
+    // their plan has radix 8 or more and at most 8 values per lane (15 interleaved rounds at
+    // radix 8: n = 1024 69.9 -> 72.8 %, 2048 68.5 -> 75.1 %, 4096 70.5 -> 77.2 % of 8 TB/s);
+    // the other plans store their bins X[k] straight from registers, runs of L values, where
+    // the extra LDS pass cost more than it saved (n = 8192 at 16 values per lane 67.8 -> 64.6 %,
+    // radix 4 at n = 1024 73.5 -> 67.0 %). Aligned = false keeps the direct store for every row
+    // of 64 lanes or more and the row-by-row staged store for the others.
     template <class P>
-    static constexpr bool direct_store() { return P::L >= 64; }
+    static constexpr bool aligned_store()
+    {
+        return Aligned && (P::L < 64 || (P::R >= 8 && P::E <= 8));
+    }
+    template <class P>
+    static constexpr bool direct_store() { return !aligned_store<P>() && P::L >= 64; }
     // The combine done by the transform's own lanes from their registers (final) for m = 8 ..
     // 64 and for rows of 16 lanes or more (X then goes back to LDS for the staged store, or out
     // directly), a separate pass over the pairs otherwise.
@@ -975,8 +1039,15 @@ struct R2cIoT {
             lds_sync<G::kWave>();
         }
         // 2. The first `keep` values of each row, stored contiguously.
-        using H = Staged<G, m + 1>;
         cf32* dst = y + first * keep;
+        if constexpr (aligned_store<P>()) {
+            if (keep == m + 1) {
+                store_run_aligned<G, m + 1, P::kStride>(lds, dst, count, tid,
+                                                        [](cf32* p, cf32 v) { put(p, v); });
+                return;
+            }
+        }
+        using H = Staged<G, m + 1>;
         H::each(count, tid, [&](int, int u, int i, bool valid) {
             if (valid && i < keep) {
                 put(dst + u * keep + i, lds[u * P::kStride + pad(i)]);
