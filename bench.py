@@ -250,11 +250,16 @@ def main(argv=None) -> int:
     extra["copy_gbps"] = round(copy_gbps, 1)
     extra["c1_pct_of_copy"] = round(100 * value / copy_gbps, 1)
     if not args.no_extra:
-        extra.update(sweep_rows(lib, impl, dev, stream))
-        extra.update(secondary_rows(args.impl, dev))
+        # Every row of this stack first; rocFFT's (through torch.fft) after all of them: rocFFT's
+        # kernels on random data slowed this stack's launches that followed them by 5-12 %.
+        later = []
         extra.update(capi_rows(lib, impl, dev, stream))
-        extra.update(navier_stokes_rows(args.impl, dev))
-        extra.update(radio_rows(args.impl, dev))
+        extra.update(sweep_rows(lib, impl, dev, stream, later))
+        extra.update(secondary_rows(args.impl, dev, later))
+        extra.update(navier_stokes_rows(args.impl, dev, later))
+        extra.update(radio_rows(args.impl, dev, later))
+        for rocfft_rows in later:
+            extra.update(rocfft_rows())
 
     line = {
         "metric": "effective HBM GB/s (% of peak) batched fp32 C2C/R2C at 2^24 points; "
@@ -286,19 +291,19 @@ def main(argv=None) -> int:
     return 0
 
 
-def secondary_rows(impl: str, dev) -> dict:
+def secondary_rows(impl: str, dev, later: list) -> dict:
     """The other configurations of the metric, each next to rocFFT (through torch.fft) on the same
     shape: C2 real transforms at n = 1024, C3 rfft2 / irfft2 at 128^2 x 1024 and 512^2 x 64 (both
-    column methods: strided, the default, and transpose), C4
-    pruned transforms on [64, 32, 128, 128] with m1 = m2 = 16, and rocFFT on the C1 shape. Inputs
-    rotate over three sets so no call reads what the previous one left in the cache."""
+    column methods: strided, the default, and transpose), C4 pruned transforms on
+    [64, 32, 128, 128] with m1 = m2 = 16, and rocFFT on the C1 shape. Inputs rotate over three
+    sets so no call reads what the previous one left in the cache. rocFFT's rows are timed by what
+    this appends to `later`, after every row of this stack."""
     import torch
 
     import spectral
     from spectral.benchmark import (fft2_modes_work, fft2_real_work, fft_real_work, time_gpu)
 
     g = torch.Generator(device=dev).manual_seed(0)
-    out = {}
 
     def timed(fn, inputs):
         k = [0]
@@ -309,38 +314,34 @@ def secondary_rows(impl: str, dev) -> dict:
 
         return time_gpu(call).median_ms
 
-    def record(name, ms, nbytes, rocfft_ms):
-        out[f"{name}_ms"] = round(ms, 5)
-        out[f"{name}_gbps"] = round(nbytes / (ms * 1e6), 1)
-        out[f"{name}_rocfft_ms"] = round(rocfft_ms, 5)
+    ours = []    # (row name, bytes, fn, inputs, rocFFT row)
+    theirs = {}  # rocFFT row -> (fn, inputs)
 
     # C2: real transforms, n = 1024, 16384 rows.
     xr = [torch.randn(16384, 1024, device=dev, generator=g) for _ in range(3)]
     xh = [torch.fft.rfft(x) for x in xr]
     work = fft_real_work(1024, 16384)[1]
-    record("c2_r2c_1024", timed(lambda x: spectral.rfft(x, impl=impl), xr), work,
-           timed(torch.fft.rfft, xr))
-    record("c2_c2r_1024", timed(lambda x: spectral.irfft(x, 1024, impl=impl), xh), work,
-           timed(lambda x: torch.fft.irfft(x, 1024), xh))
-    del xr, xh
-    # C3: 2D real transforms.
+    ours.append(("c2_r2c_1024", work, lambda x: spectral.rfft(x, impl=impl), xr, "r2c"))
+    ours.append(("c2_c2r_1024", work, lambda x: spectral.irfft(x, 1024, impl=impl), xh, "c2r"))
+    theirs["r2c"] = (torch.fft.rfft, xr)
+    theirs["c2r"] = (lambda x: torch.fft.irfft(x, 1024), xh)
+    # C3: 2D real transforms, both column methods.
     for n, arrays in ((128, 1024), (512, 64)):
         xs = [torch.randn(arrays, n, n, device=dev, generator=g) for _ in range(3)]
         hs = [torch.fft.rfft2(x) for x in xs]
         work = fft2_real_work(n, n, arrays)[1]
-        roc_f = timed(torch.fft.rfft2, xs)
-        roc_i = timed(lambda x: torch.fft.irfft2(x, s=(n, n)), hs)
-        record(f"c3_rfft2_{n}", timed(lambda x: spectral.rfft2(x, impl=impl), xs), work, roc_f)
-        record(f"c3_irfft2_{n}", timed(lambda x: spectral.irfft2(x, n, impl=impl), hs), work,
-               roc_i)
-        # BASELINE C3's second variant: the transpose method (rows, transpose, rows, transpose).
-        record(f"c3_rfft2_{n}_transpose",
-               timed(lambda x: spectral.rfft2(x, impl=impl, columns="transpose"), xs), work,
-               roc_f)
-        record(f"c3_irfft2_{n}_transpose",
-               timed(lambda x: spectral.irfft2(x, n, impl=impl, columns="transpose"), hs), work,
-               roc_i)
-        del xs, hs
+        ours.append((f"c3_rfft2_{n}", work, lambda x: spectral.rfft2(x, impl=impl), xs,
+                     f"rfft2_{n}"))
+        ours.append((f"c3_irfft2_{n}", work, lambda x, n=n: spectral.irfft2(x, n, impl=impl), hs,
+                     f"irfft2_{n}"))
+        ours.append((f"c3_rfft2_{n}_transpose", work,
+                     lambda x: spectral.rfft2(x, impl=impl, columns="transpose"), xs,
+                     f"rfft2_{n}"))
+        ours.append((f"c3_irfft2_{n}_transpose", work,
+                     lambda x, n=n: spectral.irfft2(x, n, impl=impl, columns="transpose"), hs,
+                     f"irfft2_{n}"))
+        theirs[f"rfft2_{n}"] = (torch.fft.rfft2, xs)
+        theirs[f"irfft2_{n}"] = (lambda x, n=n: torch.fft.irfft2(x, s=(n, n)), hs)
     # C4: FNO pruned transforms, [64, 32, 128, 128] <-> modes [64, 32, 32, 16].
     xp = [torch.randn(64, 32, 128, 128, device=dev, generator=g) for _ in range(3)]
     mp = [spectral.rfft2_truncated(x, 16, 16, impl=impl) for x in xp]
@@ -356,27 +357,41 @@ def secondary_rows(impl: str, dev) -> dict:
         full[..., 112:, :16] = m[..., 16:, :]
         return torch.fft.irfft2(full, s=(128, 128))
 
-    record("c4_rfft2_modes_128_m16",
-           timed(lambda x: spectral.rfft2_truncated(x, 16, 16, impl=impl), xp), work,
-           timed(rocfft_gather, xp))
-    record("c4_irfft2_modes_128_m16",
-           timed(lambda m: spectral.irfft2_from_modes(m, (128, 128), impl=impl), mp), work,
-           timed(rocfft_scatter, mp))
-    del xp, mp
+    ours.append(("c4_rfft2_modes_128_m16", work,
+                 lambda x: spectral.rfft2_truncated(x, 16, 16, impl=impl), xp, "modes_f"))
+    ours.append(("c4_irfft2_modes_128_m16", work,
+                 lambda m: spectral.irfft2_from_modes(m, (128, 128), impl=impl), mp, "modes_i"))
+    theirs["modes_f"] = (rocfft_gather, xp)
+    theirs["modes_i"] = (rocfft_scatter, mp)
     # rocFFT (through torch.fft) on the C1 shape, forward.
     xc = [torch.randn(BATCH, N, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
-    out["c1_rocfft_c2c_1024_fwd_ms"] = round(timed(torch.fft.fft, xc), 5)
+    theirs["c1"] = (torch.fft.fft, xc)
+    torch.cuda.synchronize()
+
+    out = {}
+    for name, nbytes, fn, inputs, _ in ours:
+        ms = timed(fn, inputs)
+        out[f"{name}_ms"] = round(ms, 5)
+        out[f"{name}_gbps"] = round(nbytes / (ms * 1e6), 1)
+
+    def rocfft_rows():
+        roc = {key: timed(fn, inputs) for key, (fn, inputs) in theirs.items()}
+        rows = {f"{name}_rocfft_ms": round(roc[key], 5) for name, _, _, _, key in ours}
+        rows["c1_rocfft_c2c_1024_fwd_ms"] = round(roc["c1"], 5)
+        return rows
+
+    later.append(rocfft_rows)
     return out
 
 
-def sweep_rows(lib, impl: int, dev, stream) -> dict:
+def sweep_rows(lib, impl: int, dev, stream, later: list) -> dict:
     """BASELINE C2's sweep and C1's sizes: C2C, R2C and C2R at n = 2, 4, ..., 4096 with
     batch = 2^24 / n, through the C ABI on `stream`, next to rocFFT (torch.fft) on the same shapes.
     Three buffer sets of 2^24 complex values each (384 MiB per side, 768 MiB in rotation) serve
     every size. The sizes are interleaved: each of 9 rounds times 20 launches of every (op, n),
     after 2 untimed ones, so a transient slowdown of the device lands in a round or two of each
-    row instead of all of one row's; a row reports the median round. This stack's rows are all
-    timed before rocFFT's. Rows are
+    row instead of all of one row's; a row reports the median round. rocFFT's columns are added
+    by what this appends to `later`. Rows are
     [n, us, % of 8 TB/s, rocFFT us, rocFFT %]; bytes follow the reference's convention (16 B per
     C2C point, 4n + 8(n/2 + 1) B per real row)."""
     import statistics
@@ -441,19 +456,27 @@ def sweep_rows(lib, impl: int, dev, stream) -> dict:
     # Ours over every row first, then rocFFT's: rocFFT's kernels on random data, timed between
     # ours, slowed the following launches of this stack's 1024- to 4096-point C2C by 5-12 %
     # (the same launches after rocFFT on zeros, or alone, were not slowed).
-    current = torch.cuda.current_stream(dev)
     for _ in range(9):
         for _, _, _, ours, _, us, _ in rows:
             us.append(timed_us(ours, stream))
-    for _ in range(9):
-        for _, _, _, _, theirs, _, roc in rows:
-            roc.append(timed_us(theirs, current))
     out = {"c2c": [], "r2c": [], "c2r": []}
-    for op, n, nbytes, _, _, us, roc in rows:
-        t, r = statistics.median(us), statistics.median(roc)
-        out[op].append([n, round(t, 2), round(100 * nbytes / (t * 1e3) / PEAK_GBPS, 1),
-                        round(r, 2), round(100 * nbytes / (r * 1e3) / PEAK_GBPS, 1)])
-    del ins, outs, rows
+    reported = []  # the output row of each entry of `rows`
+    for op, n, nbytes, _, _, us, _ in rows:
+        t = statistics.median(us)
+        out[op].append([n, round(t, 2), round(100 * nbytes / (t * 1e3) / PEAK_GBPS, 1)])
+        reported.append(out[op][-1])
+
+    def rocfft_columns():
+        current = torch.cuda.current_stream(dev)
+        for _ in range(9):
+            for _, _, _, _, theirs, _, roc in rows:
+                roc.append(timed_us(theirs, current))
+        for (_, _, nbytes, _, _, _, roc), row in zip(rows, reported):
+            r = statistics.median(roc)
+            row += [round(r, 2), round(100 * nbytes / (r * 1e3) / PEAK_GBPS, 1)]
+        return {}
+
+    later.append(rocfft_columns)
     return {"c2_sweep": out}
 
 
@@ -536,11 +559,12 @@ def capi_rows(lib, impl: int, dev, stream) -> dict:
     return out
 
 
-def radio_rows(impl: str, dev) -> dict:
+def radio_rows(impl: str, dev, later: list) -> dict:
     """spectral.rf as the reference's bench/bench_rf.py times it: 2^22 complex64 samples from
     seed 0, FIR of 63 and 1025 random taps (default block sizes 256 and 4096), and the Hann
     spectrum of 1024-sample frames; effective GB/s counts 16 bytes per sample (each read and
-    written once)."""
+    written once). The same operations composed on torch.fft are timed by what this appends to
+    `later`."""
     import torch
 
     from spectral import rf
@@ -551,11 +575,13 @@ def radio_rows(impl: str, dev) -> dict:
     x = torch.randn(n, dtype=torch.complex64, device=dev, generator=g)
     out = {}
 
+    theirs = []
+
     def record(name, fn_ours, fn_torch):
         ms = time_gpu(fn_ours).median_ms
         out[f"{name}_ms"] = round(ms, 5)
         out[f"{name}_gbps"] = round(16.0 * n / (ms * 1e6), 1)
-        out[f"{name}_rocfft_ms"] = round(time_gpu(fn_torch).median_ms, 5)
+        theirs.append((f"{name}_rocfft_ms", fn_torch))
 
     for m in (63, 1025):
         taps = torch.randn(m, device=dev, generator=g)
@@ -564,6 +590,7 @@ def radio_rows(impl: str, dev) -> dict:
     record("rf_spectrum1024_hann_2e22",
            lambda: rf.spectrum(x, 1024, window_name="hann", fft_impl=impl),
            lambda: rf.spectrum(x, 1024, window_name="hann", fft_impl="rocfft"))
+    later.append(lambda: {key: round(time_gpu(fn).median_ms, 5) for key, fn in theirs})
     return out
 
 
@@ -579,13 +606,13 @@ def random_vorticity(rng, n: int, batch: int, slope: float = -3.0):
     return (w / w.std(axis=(-2, -1), keepdims=True)).astype(np.float32)
 
 
-def navier_stokes_rows(impl: str, dev) -> dict:
+def navier_stokes_rows(impl: str, dev, later: list) -> dict:
     """C5: the pseudo-spectral Navier-Stokes solver (spectral.flow.gpu.GpuSolver) on 128^2 x 256
     trajectories, viscosity U[1e-3, 5e-3] per trajectory, Kolmogorov forcing sin(4y), dt 0.0025,
     a k^-3 Gaussian random initial vorticity from seed 0; one job = 32 physical frames 40 steps
     apart (1240 IMEX steps, frames kept on the GPU). Timed once per backend after 40 warm-up
-    steps: the fused stages (impl, pruned), this stack's composed pruned path, rocFFT pruned and
-    rocFFT full (the reference's torch.fft comparison)."""
+    steps: the fused stages (impl, pruned), this stack's composed pruned path, and, appended to
+    `later`, rocFFT pruned and rocFFT full (the reference's torch.fft comparison)."""
     import numpy as np
     import torch
 
@@ -598,10 +625,8 @@ def navier_stokes_rows(impl: str, dev) -> dict:
     w0 = torch.as_tensor(random_vorticity(rng, n, batch), device=dev)
     out = {}
     record = torch.empty(frames, batch, n, n, device=dev)
-    for name, kwargs in (("fused", dict(fft_impl=impl, pruned=True, fused=True)),
-                         ("composed", dict(fft_impl=impl, pruned=True, fused=False)),
-                         ("rocfft_pruned", dict(fft_impl="rocfft", pruned=True)),
-                         ("rocfft_full", dict(fft_impl="rocfft", pruned=False))):
+
+    def run(name, kwargs):
         solver = GpuSolver(n, flow, dt, device=dev, **kwargs)
         w_hat = solver.to_spectral(w0)
         for _ in range(every):
@@ -621,8 +646,13 @@ def navier_stokes_rows(impl: str, dev) -> dict:
         steps = (frames - 1) * every
         if not bool(torch.isfinite(record[-1]).all()):
             raise RuntimeError(f"C5 {name}: the solution is not finite")
-        out[f"c5_ns128_{name}_ms_per_step"] = round(1e3 * seconds / steps, 5)
-        out[f"c5_ns128_{name}_traj_steps_per_s"] = round(batch * steps / seconds)
+        return {f"c5_ns128_{name}_ms_per_step": round(1e3 * seconds / steps, 5),
+                f"c5_ns128_{name}_traj_steps_per_s": round(batch * steps / seconds)}
+
+    out.update(run("fused", dict(fft_impl=impl, pruned=True, fused=True)))
+    out.update(run("composed", dict(fft_impl=impl, pruned=True, fused=False)))
+    later.append(lambda: {**run("rocfft_pruned", dict(fft_impl="rocfft", pruned=True)),
+                          **run("rocfft_full", dict(fft_impl="rocfft", pruned=False))})
     return out
 
 
