@@ -5,15 +5,18 @@
 //
 // Design for gfx950 (wave64, LDS of 64 banks of 4 bytes, read by half-waves for 8-byte values):
 //
-// * Transposed: a workgroup of four waves moves a 64 x 64 tile of complex values. A wave reads
-//   one input row segment per step (64 lanes x 8 bytes, 512 contiguous bytes), holds all 16 of
+// * Transposed: a workgroup of eight waves moves a 64 x 64 tile of complex values. A wave reads
+//   one input row segment per step (64 lanes x 8 bytes, 512 contiguous bytes), holds all 8 of
 //   its steps' loads in registers before touching LDS (every load in flight together), then
 //   writes them to the tile; after one barrier it reads tile columns and writes output rows,
-//   again 512 contiguous bytes per wave step.
+//   again 512 contiguous bytes per wave step. Against four waves of 16 steps: 2-5 % faster on
+//   the four-step's 1024 x 16384 and on 512 x 257 spectra, equal elsewhere; 16-byte accesses
+//   (pairs of values per lane) were 7-28 % slower.
 //   The tile is unpadded and XOR-swizzled: element (p, q) sits at p * 64 + (q ^ (p mod 32)).
 //   A half-wave writing a row (fixed p, 32 consecutive q) and a half-wave reading a column
 //   (fixed q, 32 consecutive p) both cover 32 distinct 8-byte bank slots, so neither phase has a
-//   bank conflict, and the tile needs no padding column (32 KiB, five workgroups per CU).
+//   bank conflict (SQ_LDS_BANK_CONFLICT reads 0), and the tile needs no padding column (32 KiB;
+//   four workgroups of eight waves fill a CU).
 // * Not transposed: each output row is walked by a power-of-two group of lanes as wide as the row
 //   (up to a wave), so short rows (16 modes) still fill whole waves with several rows each. The
 //   row and column maps are evaluated per lane; no flat-index division per value.
@@ -25,14 +28,15 @@
 namespace spx {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;      // the row remap's workgroup
+constexpr int kTileThreads = 512;  // the transposed remap's: eight waves
 constexpr int kTile = 64;
-constexpr int kSteps = kTile / (kThreads / 64);  // tile rows per wave: 16
+constexpr int kSteps = kTile / (kTileThreads / 64);  // tile rows per wave: 8
 constexpr long long kMaxBlocks = 1 << 20;        // the loops below cover any remainder
 
 __device__ __forceinline__ cf32 zero() { return cf32{0.0f, 0.0f}; }
 
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kTileThreads)
     remap_tiles_kernel(const cf32* __restrict__ x, cf32* __restrict__ y, Remap r, int tiles_p,
                        int tiles_q, long long tiles)
 {
@@ -48,33 +52,33 @@ __global__ void __launch_bounds__(kThreads)
         const int q0 = tq * kTile;                      // output rows = input columns
         const cf32* xs = x + b * r.x_array;
 
-        // Input row rows(p) at column cols(q): lane -> q, wave + 4 k -> p.
+        // Input row rows(p) at column cols(q): lane -> q, wave + 8 k -> p.
         const int q_in = q0 + lane;
         const int xc = q_in < r.y_rows ? r.cols(q_in) : -1;
         cf32 v[kSteps];
 #pragma unroll
         for (int k = 0; k < kSteps; ++k) {
-            const int p = p0 + wave + 4 * k;
+            const int p = p0 + wave + 8 * k;
             const int xr = p < r.y_cols ? r.rows(p) : -1;
             v[k] = (xr >= 0 && xc >= 0) ? xs[static_cast<long long>(xr) * r.x_pitch + xc] : zero();
         }
 #pragma unroll
         for (int k = 0; k < kSteps; ++k) {
-            const int pl = wave + 4 * k;
+            const int pl = wave + 8 * k;
             tile[pl * kTile + (lane ^ (pl & 31))] = v[k];
         }
         __syncthreads();
-        // Output row q0 + wave + 4 k, column p0 + lane: tile column, read across p.
+        // Output row q0 + wave + 8 k, column p0 + lane: tile column, read across p.
 #pragma unroll
         for (int k = 0; k < kSteps; ++k) {
-            const int ql = wave + 4 * k;
+            const int ql = wave + 8 * k;
             v[k] = tile[lane * kTile + (ql ^ (lane & 31))];
         }
         cf32* ys = y + b * static_cast<long long>(r.y_rows) * r.y_cols;
         const int p_out = p0 + lane;
 #pragma unroll
         for (int k = 0; k < kSteps; ++k) {
-            const int q = q0 + wave + 4 * k;
+            const int q = q0 + wave + 8 * k;
             if (q < r.y_rows && p_out < r.y_cols) {
                 ys[static_cast<long long>(q) * r.y_cols + p_out] = v[k];
             }
@@ -123,8 +127,8 @@ void remap(const cf32* x, cf32* y, const Remap& r, bool transposed, hipStream_t 
         const int tiles_p = (r.y_cols + kTile - 1) / kTile;
         const int tiles_q = (r.y_rows + kTile - 1) / kTile;
         const long long tiles = static_cast<long long>(tiles_p) * tiles_q * r.batch;
-        hipLaunchKernelGGL(remap_tiles_kernel, dim3(blocks(tiles)), dim3(kThreads), 0, stream, x,
-                           y, r, tiles_p, tiles_q, tiles);
+        hipLaunchKernelGGL(remap_tiles_kernel, dim3(blocks(tiles)), dim3(kTileThreads), 0, stream,
+                           x, y, r, tiles_p, tiles_q, tiles);
     } else {
         int lanes_log2 = 0;
         while (lanes_log2 < 6 && (1 << lanes_log2) < r.y_cols) {
