@@ -722,6 +722,43 @@ struct HasFinal : std::false_type {};
 template <class Io>
 struct HasFinal<Io, std::void_t<decltype(Io::kFinal)>> : std::bool_constant<Io::kFinal> {};
 
+// A direct-input policy with `static constexpr bool kInAll = true` reads a lane's E stage-0 inputs
+// itself (in_all<P>(t, lane, v), v[b R0 + r] = element input_index<P, 0>(lane, b, r) of transform
+// t), for work shared between them (a twiddle factored over the lane's elements).
+template <class Io, class = void>
+struct HasInAll : std::false_type {};
+template <class Io>
+struct HasInAll<Io, std::void_t<decltype(Io::kInAll)>> : std::bool_constant<Io::kInAll> {};
+
+// Workgroup order across the XCDs. The dispatcher hands workgroup b to XCD b mod 8, and each XCD
+// has its own L2, so in plain order the neighbouring tiles of a strided pass (whose rows share
+// cache lines and DRAM pages) run on different XCDs. An I/O policy with
+// `static constexpr int kXcdChunk = C` renumbers each span of 8 C workgroups so that every XCD takes
+// C consecutive tiles of the span; a trailing partial span keeps its order. Spans stay short: the
+// XCDs then work on neighbouring regions, where XCDs working on regions far apart (C = grid / 8)
+// measured slower than plain order.
+template <class Io, class = void>
+struct XcdChunk : std::integral_constant<int, 0> {};
+template <class Io>
+struct XcdChunk<Io, std::void_t<decltype(Io::kXcdChunk)>>
+    : std::integral_constant<int, Io::kXcdChunk> {};
+
+template <int C>
+__device__ __forceinline__ long long xcd_order(long long b, long long grid)
+{
+    if constexpr (C == 0) {
+        return b;
+    } else {
+        constexpr long long kSpan = 8LL * C;
+        if (b >= grid / kSpan * kSpan) {
+            return b;
+        }
+        const long long base = b / kSpan * kSpan;
+        const long long r = b - base;
+        return base + (r % 8) * C + r / 8;
+    }
+}
+
 template <class P, bool Inv, bool Table, class Io>
 __global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch, const cf32* table)
 {
@@ -736,10 +773,11 @@ __global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch
     const int tid = threadIdx.x;
     const int u = tid / P::L;  // transform within the workgroup
     const int lane = tid % P::L;
-    const long long t = static_cast<long long>(blockIdx.x) * P::T + u;
+    const long long block = xcd_order<XcdChunk<Io>::value>(blockIdx.x, gridDim.x);
+    const long long t = block * P::T + u;
     const int group = tid / kGroupThreads;
     const int gtid = tid % kGroupThreads;
-    const long long group_first = static_cast<long long>(blockIdx.x) * P::T + group * kGroupT;
+    const long long group_first = block * P::T + group * kGroupT;
     const long long left = batch - group_first;
     const int group_count = left >= kGroupT ? kGroupT : (left > 0 ? static_cast<int>(left) : 0);
     cf32* const group_lds = lds + group * kGroupT * P::kStride;
@@ -748,12 +786,16 @@ __global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch
     cf32 v[P::E];
     if constexpr (Io::template direct_in<P>()) {
         if (t < batch) {
+            if constexpr (HasInAll<Io>::value) {
+                io.template in_all<P>(t, lane, v);
+            } else {
 #pragma unroll
-            for (int b = 0; b < P::E / P::template radix<0>(); ++b) {
+                for (int b = 0; b < P::E / P::template radix<0>(); ++b) {
 #pragma unroll
-                for (int r = 0; r < P::template radix<0>(); ++r) {
-                    v[b * P::template radix<0>() + r] =
-                        io.template in<P>(t, input_index<P, 0>(lane, b, r));
+                    for (int r = 0; r < P::template radix<0>(); ++r) {
+                        v[b * P::template radix<0>() + r] =
+                            io.template in<P>(t, input_index<P, 0>(lane, b, r));
+                    }
                 }
             }
         } else {
@@ -1315,13 +1357,16 @@ struct StridedIo {
     }
 };
 
-// Strided columns, persistent: workgroup b transforms the tiles of T columns b, b + gridDim.x,
-// ..., and issues each next tile's loads into registers before the current tile's stages, so
-// they are in flight during its stages and stores. Launched with as many workgroups as fit on
-// the device at once. With one tile per workgroup in flight (fft_kernel) the loads of the whole
-// device come in bursts between compute phases: at 256- and 512-point columns this measured
-// 10-13 points of the 8 TB/s peak faster on MI355X.
-template <class P, bool Inv, bool Table>
+// Strided columns, persistent: in round r workgroup b transforms the tile of T columns
+// r gridDim.x + xcd_order<C>(b), and issues each next tile's loads into registers before the
+// current tile's stages, so they are in flight during its stages and stores. Launched with as
+// many workgroups as fit on the device at once. With one tile per workgroup in flight
+// (fft_kernel) the loads of the whole device come in bursts between compute phases: at 256- and
+// 512-point columns this measured 10-13 points of the 8 TB/s peak faster on MI355X.
+// C > 0 (tiles narrower than a cache line, T = 8 at 1024 points) keeps the two tiles that share
+// each 128-byte line on one XCD: 90.8 -> 72.0 us for the 1024-point columns of 2^20-point
+// transforms (2^24 points), where 128-byte tiles gained nothing at 512 points.
+template <class P, bool Inv, bool Table, int C = 0>
 __global__ void __launch_bounds__(P::kThreads)
     columns_kernel(StridedIo io, long long batch, const cf32* table)
 {
@@ -1341,11 +1386,11 @@ __global__ void __launch_bounds__(P::kThreads)
     // forward's first pass measured 1-2 points slower with it.
     const bool nt = io.stream_out;
     cf32 val[StridedIo::steps<P>()];
-    long long tile = blockIdx.x;
-    if (tile < tiles) {
-        io.template fetch<P, false>(val, tile * P::T, count_of(tile), tid, nt);
+    const long long offset = xcd_order<C>(blockIdx.x, gridDim.x);
+    if (offset < tiles) {
+        io.template fetch<P, false>(val, offset * P::T, count_of(offset), tid, nt);
     }
-    for (; tile < tiles; tile += gridDim.x) {
+    for (long long tile = offset; tile < tiles; tile += gridDim.x) {
         const int count = count_of(tile);
         io.template park<P, false>(lds, val, count, tid);
         lds_sync<false>();

@@ -133,27 +133,30 @@ inline int device_cus()
 // The persistent strided column kernel over as many workgroups as fit on the device at once.
 // Workgroups per CU depend only on the kernel and the architecture (gfx950 everywhere this
 // library runs), so the first query serves every device; the CU count is per device.
-template <class P, bool Inv, bool Table>
+template <class P, bool Inv, bool Table, int C = 0>
 void launch_columns_persistent(const StridedIo& io, long long batch, hipStream_t stream)
 {
     static const int per_cu = [] {
         int blocks = 0;
         const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &blocks, reinterpret_cast<const void*>(&columns_kernel<P, Inv, Table>), P::kThreads,
-            0);
+            &blocks, reinterpret_cast<const void*>(&columns_kernel<P, Inv, Table, C>),
+            P::kThreads, 0);
         return e == hipSuccess && blocks > 0 ? blocks : 1;
     }();
     const long long tiles = (batch + P::T - 1) / P::T;
     const long long grid = std::min(tiles, static_cast<long long>(device_cus()) * per_cu);
     const cf32* table = Table ? twiddle_table() : nullptr;
-    hipLaunchKernelGGL((columns_kernel<P, Inv, Table>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((columns_kernel<P, Inv, Table, C>), dim3(static_cast<unsigned>(grid)),
                        dim3(P::kThreads), 0, stream, io, batch, table);
     SPX_LAUNCH_CHECK();
 }
 
-// Strided columns of the 16-column tiles at 256 and 512 points run persistent (columns_kernel);
-// other lengths keep one tile per workgroup (persistent measured 2-3 points faster at 128 and 1-2
-// slower at 1024, whose tiles hold 8 columns).
+// Strided columns of 256, 512 and 1024 points run persistent (columns_kernel); other lengths keep
+// one tile per workgroup (persistent measured 2-3 points faster at 128). The 1024-point tiles hold
+// 8 columns of 16 values per lane, one wave per column (workgroups of 512 lanes), in XCD order:
+// 72.0 us for the columns of 2^20-point transforms over 2^24 points on MI355X, against 90.8 us for
+// one tile per workgroup of 1024 lanes (8 values per lane, two waves per column) and 85.3 us for
+// the same persistent kernel in plain order.
 template <int R, bool Inv, bool Table>
 void dispatch_strided_columns(int n, const StridedIo& io, long long batch, hipStream_t stream)
 {
@@ -165,6 +168,9 @@ void dispatch_strided_columns(int n, const StridedIo& io, long long batch, hipSt
     case 512:
         launch_columns_persistent<Plan<512, R, column_e<512, R>(), column_threads<512, R>()>, Inv,
                                   Table>(io, batch, stream);
+        break;
+    case 1024:
+        launch_columns_persistent<Plan<1024, R, 16, 512>, Inv, Table, 32>(io, batch, stream);
         break;
     default:
         dispatch_columns<R, Inv, Table>(n, io, batch, stream);
@@ -232,6 +238,48 @@ struct TwiddleRowsIo {
         return twiddled(t, i, x[t * P::N + i]);
     }
 
+    // A lane's stage-0 elements are i = lane + L m, m = b + r E / R0 < E, so the twiddle factors:
+    // w^(k1 i) = w^(k1 lane) w^(k1 L m). When a wave lies inside one transform (L >= 64: k1 is the
+    // same on all its lanes) lane j computes w^(k1 L j) and every lane reads factor m from lane m:
+    // two sincospi per lane instead of E. Both angles are exact in float (k1 L m < n1 N <= 2^24).
+    static constexpr bool kInAll = true;
+    template <class P>
+    __device__ __forceinline__ void in_all(long long t, int lane, cf32 (&v)[P::E]) const
+    {
+        constexpr int R0 = P::template radix<0>();
+        const cf32* const row = x + t * P::N;
+        if constexpr (P::L >= 64 && P::E <= 64) {
+            const int k1 = static_cast<int>(t & (n1 - 1));
+            const int j = static_cast<int>(threadIdx.x & 63) % P::E;
+            const cf32 base = expi_pi(static_cast<float>(k1 * lane) * two_over_n);
+            const cf32 step = expi_pi(static_cast<float>(k1 * P::L * j) * two_over_n);
+#pragma unroll
+            for (int b = 0; b < P::E / R0; ++b) {
+#pragma unroll
+                for (int r = 0; r < R0; ++r) {
+                    constexpr int kPerR = P::E / R0;
+                    const int m = b + r * kPerR;
+                    const cf32 f{__builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                     __builtin_bit_cast(int, step.re), m)),
+                                 __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                     __builtin_bit_cast(int, step.im), m))};
+                    cf32 w = cmul(base, f);
+                    w.im *= sign;
+                    v[b * R0 + r] = cmul(row[lane + P::L * m], w);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < P::E / R0; ++b) {
+#pragma unroll
+                for (int r = 0; r < R0; ++r) {
+                    const int i = input_index<P, 0>(lane, b, r);
+                    v[b * R0 + r] = twiddled(t, i, row[i]);
+                }
+            }
+        }
+    }
+
     template <class P>
     __device__ __forceinline__ void out(long long t, int i, cf32 v) const
     {
@@ -278,6 +326,12 @@ struct TwiddleRowsTransposedIo {
 
     template <class P>
     __device__ __forceinline__ cf32 in(long long t, int i) const { return rows.in<P>(t, i); }
+    static constexpr bool kInAll = true;
+    template <class P>
+    __device__ __forceinline__ void in_all(long long t, int lane, cf32 (&v)[P::E]) const
+    {
+        rows.in_all<P>(t, lane, v);
+    }
     template <class P>
     __device__ __forceinline__ void out(long long, int, cf32) const {}
 
@@ -411,10 +465,15 @@ struct ColumnStepIo {
     }
 };
 
-// Rows of the two-pass split: 1024 lanes holding 16 rows (of 512 or 1024 points), so the
-// transposed store writes 128-byte runs.
+// Rows of the two-pass split: 1024 lanes holding 16 rows of 512 points or 8 rows of 1024, so
+// the transposed store writes 128- or 64-byte runs. At 1024 points 8 rows (64 KiB of LDS, two
+// workgroups per CU) measured 64.3 us over 2^24 points on MI355X against 67.2 us for 16 rows
+// (128 KiB, one workgroup per CU).
+template <int N>
+constexpr int transposed_rows() { return N <= 512 ? 16 : 8; }
 template <int N, int R>
-using TransposedRowsPlan = Plan<N, R, cmax(cmax(R, 4), N * 16 / kMaxBlock), kMaxBlock>;
+using TransposedRowsPlan =
+    Plan<N, R, cmax(cmax(R, 4), N * transposed_rows<N>() / kMaxBlock), kMaxBlock>;
 
 }  // namespace dev
 
