@@ -168,6 +168,208 @@ __device__ __forceinline__ void row_c2r(const cf32* src, cf32* s, cf32 (&v)[NP::
     lds_sync<true>();  // every lane is done with s before it is reused
 }
 
+// --- two real fields per complex transform --------------------------------------------------
+//
+// The same stage with the four derived fields taken in the pairs whose products form the
+// nonlinear term, (u, wx) and then (v, wy). Inverse: the column transforms of both fields of a
+// pair in one pass (2m of the N column slots), then per grid row ONE N-point complex inverse of
+// Z = A + i B: for real A and B the row spectrum of Z is A~ + i B~ at kx >= 0 and
+// conj(A~) + i conj(B~) at -kx, and A B = Re z Im z in registers. Forward: per row the N-point
+// complex transform of the product (imaginary part zero), its first m bins, then the m forward
+// columns. That is half the column and row phases of the field-at-a-time kernel. The state is
+// read from global memory (L2 after the first column pass), so the LDS holds only the tile, and
+// each row group uses its own tile row as exchange scratch.
+template <int N_, int R, int E>
+struct NsPairPlan {
+    static constexpr int N = N_;
+    static constexpr int m = N / 3 + 1;              // kept modes per axis
+    static constexpr int rows = 2 * m;                // kept rows
+    using PX = Plan<N, R, E>;                         // rows and columns: N-point complex
+    static constexpr int NT = N * PX::L;              // one lane group per grid row
+    static constexpr int RS = (pad(N - 1) + 1) | 1;   // tile row stride: a padded row, odd
+    static constexpr int kLds = N * RS;
+    static constexpr int kW = rows * m;
+
+    static_assert(PX::L <= 64 && 64 % PX::L == 0, "a row's or a column's lanes in one wave");
+    static_assert(NT <= 1024, "one workgroup");
+    static_assert(NT / PX::L >= 2 * m && RS >= 2 * m, "both fields' columns in one pass");
+    static_assert(slots_match<PX>(), "inverse outputs must be forward inputs");
+    static_assert(kLds * sizeof(cf32) <= 160 * 1024, "LDS budget");
+};
+
+// Inverse column transforms of the pair's two derived fields into tile columns 0 .. m-1 (first)
+// and m .. 2m-1 (second).
+template <class NP>
+__device__ __forceinline__ void pair_columns(const cf32* __restrict__ w, cf32* T, int pair,
+                                             int tid)
+{
+    using PX = typename NP::PX;
+    constexpr int R0 = PX::template radix<0>();
+    const int slot = tid / PX::L;
+    const int lane = tid % PX::L;
+    if (slot < 2 * NP::m) {
+        // Derived field d = i f w with a real multiplier f per mode: u = i (ky / k^2) w,
+        // wx = i kx w (pair 0); v = i (-kx / k^2) w, wy = i ky w (pair 1).
+        const bool second = slot >= NP::m;
+        const int c = second ? slot - NP::m : slot;
+        const float kx = static_cast<float>(c);
+        const bool on_ky = (pair == 0) != second;  // u and wy take ky, wx and v take kx
+        const bool by_k2 = !second;                // u and v divide by |k|^2
+        const float sign = (pair == 1 && !second) ? -1.0f : 1.0f;
+        cf32 v[PX::E];
+#pragma unroll
+        for (int b = 0; b < PX::E / R0; ++b) {
+#pragma unroll
+            for (int r = 0; r < R0; ++r) {
+                const int mr = mode_row<NP>(input_index<PX, 0>(lane, b, r));
+                cf32 d = czero();
+                if (mr >= 0) {
+                    const cf32 wv = w[mr * NP::m + c];
+                    const float ky = ky_of_mode_row<NP>(mr);
+                    const float k2 = kx * kx + ky * ky;
+                    float f = sign * (on_ky ? ky : kx);
+                    if (by_k2) {
+                        f = k2 > 0.0f ? f / k2 : 0.0f;
+                    }
+                    d = mul_ik(f, wv);
+                }
+                v[b * R0 + r] = d;
+            }
+        }
+        cf32* const s = T + slot;
+        run_stages<PX, 0, true, false, Strided<NP::RS>>(v, s, lane, nullptr);
+        lds_sync<true>();
+        final_write<PX, Strided<NP::RS>>(s, v, lane);
+    }
+}
+
+// Grid row y's inverse of Z = A + i B from its tile row (A~ in columns 0 .. m-1, B~ in
+// m .. 2m-1), scaled by `scale`: on return v holds z at the last stage's slots. The DC bins'
+// imaginary parts are dropped (numpy's irfft does the same). The tile row is the exchange
+// scratch: run_stages waits for the row group's reads before its first write.
+template <class NP>
+__device__ __forceinline__ void pair_row_inverse(cf32* row, cf32 (&v)[NP::PX::E], int lane,
+                                                 float scale)
+{
+    using PX = typename NP::PX;
+    constexpr int R0 = PX::template radix<0>();
+    static_for<0, PX::E>([&](auto ei) {
+        constexpr int e = decltype(ei)::value;
+        constexpr int off = (e / R0) * PX::L + (e % R0) * (PX::N / R0);
+        const int k = lane + off;
+        cf32 z = czero();
+        if (k < NP::m) {
+            cf32 a = row[k];
+            cf32 b = row[NP::m + k];
+            if (k == 0) {
+                a.im = 0.0f;
+                b.im = 0.0f;
+            }
+            z = cf32{a.re - b.im, a.im + b.re};
+        } else if (k > NP::N - NP::m) {
+            const cf32 a = row[NP::N - k];
+            const cf32 b = row[NP::m + NP::N - k];
+            z = cf32{a.re + b.im, b.re - a.im};
+        }
+        v[e] = cscale(z, scale);
+    });
+    run_stages<PX, 0, true, false>(v, row, lane, nullptr);
+}
+
+template <class NP>
+__global__ void __launch_bounds__(NP::NT)
+    ns_pair_kernel(const cf32* __restrict__ state, const cf32* __restrict__ w0,
+                   const cf32* __restrict__ f0, cf32* __restrict__ out_f,
+                   cf32* __restrict__ out_w, const cf32* __restrict__ forcing_hat,
+                   const float* __restrict__ nu, int nu_stride, float drag, float dt, int stage)
+{
+    using PX = typename NP::PX;
+    __shared__ cf32 T[NP::kLds];
+    const int tid = threadIdx.x;
+    const long long field = blockIdx.x;
+    const long long base = field * NP::kW;
+    const cf32* const w = state + base;
+    const int lane = tid % PX::L;
+    cf32* const row = T + (tid / PX::L) * NP::RS;  // this lane group's grid row
+    constexpr float kScale = 1.0f / (static_cast<float>(NP::N) * static_cast<float>(NP::N));
+
+    // u wx + v wy: per pair, both fields' columns into T, then each row's packed inverse.
+    // Both pairs unrolled (the pair then known at compile time): 121 VGPRs and no spills at
+    // n = 128, where the loop kept at run time spilled 32 bytes per lane.
+    float nl[PX::E];
+#pragma unroll
+    for (int pair = 0; pair < 2; ++pair) {
+        pair_columns<NP>(w, T, pair, tid);
+        __syncthreads();
+        cf32 v[PX::E];
+        pair_row_inverse<NP>(row, v, lane, kScale);
+#pragma unroll
+        for (int e = 0; e < PX::E; ++e) {
+            const float p = v[e].re * v[e].im;
+            nl[e] = pair == 0 ? p : nl[e] + p;
+        }
+        __syncthreads();  // every row group is done with its tile row before the next columns
+    }
+
+    // Forward row transforms of the product, the first m bins into the tile row.
+    {
+        cf32 v[PX::E];
+        static_for<0, PX::E>([&](auto ei) {
+            constexpr int e = decltype(ei)::value;
+            v[forward_slot_of<PX>(e)] = cf32{nl[e], 0.0f};
+        });
+        run_stages<PX, 0, false, false>(v, row, lane, nullptr);
+        lds_sync<true>();  // the row group's last exchange reads are done
+        constexpr int RL = PX::template radix<PX::kStages - 1>();
+        static_for<0, PX::E>([&](auto ei) {
+            constexpr int e = decltype(ei)::value;
+            const int k = lane + (e / RL) * PX::L + (e % RL) * (PX::N / RL);
+            if (k < NP::m) {
+                row[k] = v[e];
+            }
+        });
+    }
+    __syncthreads();
+
+    // Forward columns of the product's row spectra, in place in T.
+    {
+        const int c = tid / PX::L;
+        if (c < NP::m) {
+            cf32* const col = T + c;
+            cf32 v[PX::E];
+            stage_read<PX, 0, Strided<NP::RS>>(col, v, lane);
+            run_stages<PX, 0, false, false, Strided<NP::RS>>(v, col, lane, nullptr);
+            lds_sync<true>();
+            final_write<PX, Strided<NP::RS>>(col, v, lane);
+        }
+    }
+    __syncthreads();
+
+    // Epilogue on the kept modes.
+    const float nu_f = nu[field * nu_stride];
+    const float kmax = static_cast<float>(NP::N) / 3.0f;
+    for (int e = tid; e < NP::kW; e += NP::NT) {
+        const int r = e / NP::m;
+        const int c = e - r * NP::m;
+        const float ky = ky_of_mode_row<NP>(r);
+        const float kx = static_cast<float>(c);
+        const int i = r < NP::m ? r : r - 2 * NP::m + NP::N;
+        const bool kept = fabsf(kx) <= kmax && fabsf(ky) <= kmax;
+        const cf32 nlh = kept ? T[i * NP::RS + c] : czero();
+        const cf32 F = csub(forcing_hat[e], nlh);
+        const float linear = -nu_f * (kx * kx + ky * ky) - drag;
+        const float ex = 1.0f + 0.5f * dt * linear;
+        const float im = 1.0f / (1.0f - 0.5f * dt * linear);
+        if (stage == 0) {
+            out_f[base + e] = F;
+            out_w[base + e] = cscale(cadd(cscale(w[e], ex), cscale(F, dt)), im);
+        } else {
+            const cf32 sum = cadd(f0[base + e], F);
+            out_w[base + e] = cscale(cadd(cscale(w0[base + e], ex), cscale(sum, 0.5f * dt)), im);
+        }
+    }
+}
+
 template <class NP>
 __global__ void __launch_bounds__(NP::NT)
     ns_stage_kernel(const cf32* __restrict__ state, const cf32* __restrict__ w0,
@@ -303,8 +505,8 @@ void launch(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32
     // (1024 lanes) took 34.8 us; radix 16 or 16 values per lane (fewer exchanges, 512 lanes, or
     // spills at 1024) took 37.6-41.8 us. At n = 64, radix 4 with 4 values per lane (512 lanes)
     // took 14.8 us against 16.8 us for radix 8 (256 lanes).
-    using NP = std::conditional_t<N == 64, NsPlan<64, 4, 4, 4, 4>, NsPlan<N, 8, 8, 8, 8>>;
-    hipLaunchKernelGGL(ns_stage_kernel<NP>, dim3(static_cast<unsigned>(batch)), dim3(NP::NT), 0,
+    using NP = std::conditional_t<N == 64, NsPairPlan<64, 8, 8>, NsPairPlan<N, 16, 16>>;
+    hipLaunchKernelGGL(ns_pair_kernel<NP>, dim3(static_cast<unsigned>(batch)), dim3(NP::NT), 0,
                        stream, state, w0, f0, out_f, out_w, forcing_hat, nu, nu_stride, drag, dt,
                        stage);
     SPX_LAUNCH_CHECK();
