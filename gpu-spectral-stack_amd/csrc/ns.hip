@@ -7,24 +7,30 @@
 // State: omega_hat on the 2/3-rule modes in the layout of rfft2_truncated with m = n/3 + 1 (rows
 // ky = 0 .. m-1 then -m .. -1, columns kx = 0 .. m-1), (2m) x m complex values per field.
 //
-// Per field (one workgroup, one lane group per grid row and per kept column):
-//   load W = omega_hat (LDS)
-//   for each derived field d = u = i ky psi_hat, wx = i kx omega_hat, v = -i kx psi_hat,
-//   wy = i ky omega_hat (psi_hat = omega_hat / |k|^2), one at a time through one tile T
-//   (n rows x m columns):
-//     columns: the inverse column transforms of d's m kept columns into T (one pass)
-//     rows:    per grid row, the c2r of T's row into registers (one pass); the products u wx
-//              and then v wy accumulate in registers
-//   forward: per row, the r2c of the product (still in registers), its first m bins into T;
-//   then the forward transforms of T's m columns, and the epilogue on the kept modes:
+// Per field (one workgroup; one lane group per grid row, and per column in the column phases):
+//   nonlinear term N = u wx + v wy with u = i ky psi_hat, v = -i kx psi_hat, wx = i kx omega_hat,
+//   wy = i ky omega_hat (psi_hat = omega_hat / |k|^2), two real fields per complex transform:
+//     for each pair (A, B) = (u, wx), then (v, wy):
+//       columns: the inverse column transforms of A's and B's m kept columns into the tile T
+//                (2m of the n column slots, one pass)
+//       rows:    per grid row ONE n-point complex inverse of Z = A + i B: for real A and B the
+//                row spectrum of Z is A~ + i B~ at kx >= 0 and conj(A~) + i conj(B~) at -kx, and
+//                A B = Re z Im z in registers
+//   forward: per row the n-point complex transform of N (imaginary part zero), its first m bins
+//   into T; then the m forward column transforms, and the epilogue on the kept modes:
 //           F = f_hat - mask N_hat, and the IMEX update
 //             stage 0: out_f = F, out_w = w* = (e w + dt F) i
 //             stage 1: out_w = w' = (e w + dt/2 (f0 + F)) i
 //           with e = 1 + dt/2 L, i = 1 / (1 - dt/2 L), L = -nu |k|^2 - alpha.
-// One field at a time keeps the LDS to W, T and a scratch row per grid row (144 KB at n = 128),
-// so every row phase and every column phase is a single pass of the workgroup: the stage is a
-// chain of dependent LDS passes, and their number is what sets its time.
+// The state is read from global memory (L2 after the first column pass), so the LDS holds only
+// the tile, and each row group uses its own tile row as exchange scratch.
 // Normalization: inverse 1 / n^2 over the column and row passes, forward none, as numpy.
+//
+// Measured on MI355X (n = 128, 256 fields, one stage): 31.2 us for the field-at-a-time form
+// (four inverse column and four real row phases), 26.2 us with the fields paired, 18.8 us with
+// the tile below free of bank conflicts (62 % of LDS cycles were conflicts). The stage is bound
+// by its chain of dependent phases on one CU per field (the batch equals the CU count) and
+// within them by VALU issue (80 % of a SIMD's cycles).
 
 #include "stockham.hpp"
 
@@ -35,30 +41,6 @@
 namespace spx {
 namespace dev {
 namespace {
-
-template <int N_, int RR = 8, int ER = 8, int RC = 8, int EC = 8>
-struct NsPlan {
-    static constexpr int N = N_;
-    static constexpr int M = N / 2;         // complex values per real row
-    static constexpr int m = N / 3 + 1;      // kept modes per axis
-    static constexpr int rows = 2 * m;       // kept rows
-    static constexpr int TS = m | 1;         // tile row stride (odd: columns hit distinct banks)
-    using PR = Plan<M, RR, ER>;              // row transforms (M-point complex)
-    using PC = Plan<N, RC, EC>;              // column transforms
-    static constexpr int NT = N * PR::L;     // one lane group per grid row
-    static constexpr int CPP = NT / PC::L;   // columns per pass
-    static constexpr int RS = (pad(M) + 1) | 1;  // scratch row stride
-    // LDS layout, in complex values: W, the tile, a scratch row per grid row
-    static constexpr int kW = rows * m;
-    static constexpr int kT = N * TS;
-    static constexpr int kS = N * RS;
-    static constexpr int kLds = kW + kT + kS;
-
-    static_assert(PR::L <= 64 && PC::L <= 64, "wave-local transforms");
-    static_assert(NT <= 1024, "one workgroup");
-    static_assert(CPP >= m, "one column pass per field");
-    static_assert(kLds * sizeof(cf32) <= 160 * 1024, "LDS budget");
-};
 
 __device__ __forceinline__ cf32 mul_ik(float k, cf32 z) { return {-k * z.im, k * z.re}; }
 
@@ -81,105 +63,6 @@ __device__ __forceinline__ float ky_of_mode_row(int r)
     return static_cast<float>(r < NP::m ? r : r - 2 * NP::m);
 }
 
-// The spectrum of derived field `which` at kept mode (r, c) from W (omega_hat):
-//   0: u = i ky psi,  1: wx = i kx omega,  2: v = -i kx psi,  3: wy = i ky omega.
-template <class NP>
-__device__ __forceinline__ cf32 derived(const cf32* W, int r, int c, int which)
-{
-    const cf32 w = W[r * NP::m + c];
-    const float ky = ky_of_mode_row<NP>(r);
-    const float kx = static_cast<float>(c);
-    const float k2 = kx * kx + ky * ky;
-    const float inv_k2 = k2 > 0.0f ? 1.0f / k2 : 0.0f;
-    switch (which) {
-    case 0:
-        return mul_ik(ky, cscale(w, inv_k2));
-    case 1:
-        return mul_ik(kx, w);
-    case 2:
-        return mul_ik(-kx, cscale(w, inv_k2));
-    default:
-        return mul_ik(ky, w);
-    }
-}
-
-// Inverse column transforms of derived field `which` (its m kept columns) into T.
-template <class NP>
-__device__ __forceinline__ void inverse_columns(const cf32* W, cf32* T, int which, int tid)
-{
-    using PC = typename NP::PC;
-    constexpr int R0 = PC::template radix<0>();
-    const int c = tid / PC::L;
-    const int lane = tid % PC::L;
-    if (c < NP::m) {
-        cf32 v[PC::E];
-#pragma unroll
-        for (int b = 0; b < PC::E / R0; ++b) {
-#pragma unroll
-            for (int r = 0; r < R0; ++r) {
-                const int mr = mode_row<NP>(input_index<PC, 0>(lane, b, r));
-                v[b * R0 + r] = mr >= 0 ? derived<NP>(W, mr, c, which) : czero();
-            }
-        }
-        cf32* const s = T + c;
-        run_stages<PC, 0, true, false, Strided<NP::TS>>(v, s, lane, nullptr);
-        lds_sync<true>();
-        final_write<PC, Strided<NP::TS>>(s, v, lane);
-    }
-}
-
-// Real inverse of tile row `src` (m nonzero bins) for one row: each lane forms the prepared values
-// of its own first-stage inputs straight from the tile row, Z[k] = ev + i d w^k with ev, d from
-// X[k] and conj(X[M-k]) and w = exp(i pi / M), then runs the M-point inverse transform (s is its
-// exchange scratch); on return v holds the row's reals as complex pairs, in the last stage's
-// slots, scaled by `scale`. A lane's inputs are k = lane + q L (q < E), so its twiddles are
-// w^lane times compile-time constants.
-template <class NP>
-__device__ __forceinline__ void row_c2r(const cf32* src, cf32* s, cf32 (&v)[NP::PR::E], int lane,
-                                        float scale)
-{
-    using PR = typename NP::PR;
-    constexpr int M = NP::M;
-    constexpr int R0 = PR::template radix<0>();
-    static_assert(M >= NP::m, "X[M] (Nyquist) lies outside the kept bins");
-    const cf32 base = twiddle_of<2 * M, true>(lane);
-    static_for<0, PR::E>([&](auto ei) {
-        constexpr int e = decltype(ei)::value;
-        constexpr int b = e / R0;
-        constexpr int r = e % R0;
-        constexpr int off = b * PR::L + r * (PR::N / R0);  // k = lane + off
-        const int k = lane + off;
-        cf32 xk = k < NP::m ? src[k] : czero();
-        const cf32 xm = (k > 0 && M - k < NP::m) ? src[M - k] : czero();
-        if (k == 0) {
-            xk.im = 0.0f;
-        }
-        const cf32 ev{0.5f * (xk.re + xm.re), 0.5f * (xk.im - xm.im)};
-        const cf32 d{0.5f * (xk.re - xm.re), 0.5f * (xk.im + xm.im)};
-        constexpr cf32 c = const_twiddle<true>(off, 2 * M);
-        const cf32 od = cmul(d, off == 0 ? base : cmul(base, c));
-        v[e] = cf32{ev.re - od.im, ev.im + od.re};
-    });
-    run_stages<PR, 0, true, false>(v, s, lane, nullptr);
-#pragma unroll
-    for (int e = 0; e < PR::E; ++e) {
-        v[e] = cscale(v[e], scale);
-    }
-    lds_sync<true>();  // every lane is done with s before it is reused
-}
-
-// --- two real fields per complex transform --------------------------------------------------
-//
-// The same stage with the four derived fields taken in the pairs whose products form the
-// nonlinear term, (u, wx) and then (v, wy). Inverse: the column transforms of both fields of a
-// pair in one pass (2m of the N column slots), then per grid row ONE N-point complex inverse of
-// Z = A + i B: for real A and B the row spectrum of Z is A~ + i B~ at kx >= 0 and
-// conj(A~) + i conj(B~) at -kx, and A B = Re z Im z in registers. Forward: per row the N-point
-// complex transform of the product (imaginary part zero), its first m bins, then the m forward
-// columns. That is half the column and row phases of the field-at-a-time kernel. The state is
-// read from global memory (L2 after the first column pass), so the LDS holds only the tile, and
-// each row group uses its own tile row as exchange scratch.
-//
 // Tile layout, free of LDS bank conflicts (64 banks of 4 bytes, 8-byte accesses served a
 // half-wave at a time): grid row y sits in tile row pad(y) (one spare row after every 16), tile
 // rows are RS = 8 mod 32 values apart, and a column's lanes are spread over the wave (lane j of
@@ -258,7 +141,7 @@ __device__ __forceinline__ void pair_columns(const cf32* __restrict__ w, cf32* T
                     const float k2 = kx * kx + ky * ky;
                     float f = sign * (on_ky ? ky : kx);
                     if (by_k2) {
-                        f = k2 > 0.0f ? f / k2 : 0.0f;
+                        f = k2 > 0.0f ? f * __builtin_amdgcn_rcpf(k2) : 0.0f;
                     }
                     d = mul_ik(f, wv);
                 }
@@ -307,7 +190,7 @@ __device__ __forceinline__ void pair_row_inverse(cf32* row, cf32 (&v)[NP::PX::E]
 
 template <class NP>
 __global__ void __launch_bounds__(NP::NT)
-    ns_pair_kernel(const cf32* __restrict__ state, const cf32* __restrict__ w0,
+    ns_stage_kernel(const cf32* __restrict__ state, const cf32* __restrict__ w0,
                    const cf32* __restrict__ f0, cf32* __restrict__ out_f,
                    cf32* __restrict__ out_w, const cf32* __restrict__ forcing_hat,
                    const float* __restrict__ nu, int nu_stride, float drag, float dt, int stage)
@@ -401,143 +284,15 @@ __global__ void __launch_bounds__(NP::NT)
     }
 }
 
-template <class NP>
-__global__ void __launch_bounds__(NP::NT)
-    ns_stage_kernel(const cf32* __restrict__ state, const cf32* __restrict__ w0,
-                    const cf32* __restrict__ f0, cf32* __restrict__ out_f,
-                    cf32* __restrict__ out_w, const cf32* __restrict__ forcing_hat,
-                    const float* __restrict__ nu, int nu_stride, float drag, float dt, int stage)
-{
-    using PR = typename NP::PR;
-    using PC = typename NP::PC;
-    static_assert(slots_match<PR>(), "row inverse outputs must be the row forward's inputs");
-    __shared__ cf32 lds[NP::kLds];
-    cf32* const W = lds;
-    cf32* const T = W + NP::kW;
-    cf32* const S = T + NP::kT;
-
-    const int tid = threadIdx.x;
-    const long long field = blockIdx.x;
-    const long long base = field * NP::kW;
-
-    // Load the state's modes.
-    for (int e = tid; e < NP::kW; e += NP::NT) {
-        W[e] = state[base + e];
-    }
-    __syncthreads();
-
-    constexpr float kInvScale = 1.0f / static_cast<float>(NP::N * NP::M);
-    const int y = tid / PR::L;  // this lane group's grid row
-    const int rlane = tid % PR::L;
-    cf32* const s = S + y * NP::RS;
-    cf32* const trow = T + y * NP::TS;
-
-    // u wx + v wy, one derived field at a time: columns into T, then each row's c2r.
-    cf32 nl[PR::E];
-    cf32 first[PR::E];
-#pragma unroll 1
-    for (int which = 0; which < 4; ++which) {
-        inverse_columns<NP>(W, T, which, tid);
-        __syncthreads();
-        cf32 v[PR::E];
-        row_c2r<NP>(trow, s, v, rlane, kInvScale);
-        if (which == 0 || which == 2) {
-#pragma unroll
-            for (int e = 0; e < PR::E; ++e) {
-                first[e] = v[e];
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < PR::E; ++e) {
-                const cf32 p{first[e].re * v[e].re, first[e].im * v[e].im};
-                nl[e] = which == 1 ? p : cf32{nl[e].re + p.re, nl[e].im + p.im};
-            }
-        }
-        __syncthreads();  // every row has read T before the next field's columns overwrite it
-    }
-
-    // Forward row transform of the product, its first m bins into T.
-    {
-        cf32 v[PR::E];
-        static_for<0, PR::E>([&](auto ei) {
-            constexpr int e = decltype(ei)::value;
-            v[forward_slot_of<PR>(e)] = nl[e];
-        });
-        run_stages<PR, 0, false, false>(v, s, rlane, nullptr);
-        lds_sync<true>();
-        final_write<PR>(s, v, rlane);
-        lds_sync<true>();
-        constexpr int M = NP::M;
-        for (int k = rlane; k <= M / 2; k += PR::L) {
-            const cf32 zk = s[pad(k & (M - 1))];
-            const cf32 zm = s[pad((M - k) & (M - 1))];
-            const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
-            const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
-            const cf32 wo = cmul(twiddle_of<2 * M, false>(k), od);
-            if (k < NP::m) {
-                trow[k] = cadd(ev, wo);
-            }
-            if (k < M - k && M - k < NP::m) {
-                trow[M - k] = cconj(csub(ev, wo));
-            }
-        }
-    }
-    __syncthreads();
-
-    // Forward columns of the product's row spectra, in place in T.
-    {
-        const int c = tid / PC::L;
-        const int lane = tid % PC::L;
-        if (c < NP::m) {
-            cf32* const col = T + c;
-            cf32 v[PC::E];
-            stage_read<PC, 0, Strided<NP::TS>>(col, v, lane);
-            run_stages<PC, 0, false, false, Strided<NP::TS>>(v, col, lane, nullptr);
-            lds_sync<true>();
-            final_write<PC, Strided<NP::TS>>(col, v, lane);
-        }
-    }
-    __syncthreads();
-
-    // Epilogue on the kept modes.
-    const float nu_f = nu[field * nu_stride];
-    const float kmax = static_cast<float>(NP::N) / 3.0f;
-    for (int e = tid; e < NP::kW; e += NP::NT) {
-        const int r = e / NP::m;
-        const int c = e - r * NP::m;
-        const float ky = ky_of_mode_row<NP>(r);
-        const float kx = static_cast<float>(c);
-        const int i = r < NP::m ? r : r - 2 * NP::m + NP::N;
-        const bool kept = fabsf(kx) <= kmax && fabsf(ky) <= kmax;
-        const cf32 nlh = kept ? T[i * NP::TS + c] : czero();
-        const cf32 fh = forcing_hat[e];
-        const cf32 F = csub(fh, nlh);
-        const float linear = -nu_f * (kx * kx + ky * ky) - drag;
-        const float ex = 1.0f + 0.5f * dt * linear;
-        const float im = 1.0f / (1.0f - 0.5f * dt * linear);
-        if (stage == 0) {
-            const cf32 w = W[e];
-            out_f[base + e] = F;
-            out_w[base + e] = cscale(cadd(cscale(w, ex), cscale(F, dt)), im);
-        } else {
-            const cf32 w = w0[base + e];
-            const cf32 sum = cadd(f0[base + e], F);
-            out_w[base + e] = cscale(cadd(cscale(w, ex), cscale(sum, 0.5f * dt)), im);
-        }
-    }
-}
-
 template <int N>
 void launch(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32* out_w,
             const cf32* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
             int batch, int stage, hipStream_t stream)
 {
-    // Measured on MI355X (one stage, 256 fields): at n = 128, radix 8 with 8 values per lane
-    // (1024 lanes) took 34.8 us; radix 16 or 16 values per lane (fewer exchanges, 512 lanes, or
-    // spills at 1024) took 37.6-41.8 us. At n = 64, radix 4 with 4 values per lane (512 lanes)
-    // took 14.8 us against 16.8 us for radix 8 (256 lanes).
+    // n = 128: radix 16 then 8, 16 values per lane (1024 lanes); n = 64: radix 8 twice, 8 values
+    // per lane (512 lanes). Both are two-stage transforms, one LDS exchange each.
     using NP = std::conditional_t<N == 64, NsPairPlan<64, 8, 8>, NsPairPlan<N, 16, 16>>;
-    hipLaunchKernelGGL(ns_pair_kernel<NP>, dim3(static_cast<unsigned>(batch)), dim3(NP::NT), 0,
+    hipLaunchKernelGGL(ns_stage_kernel<NP>, dim3(static_cast<unsigned>(batch)), dim3(NP::NT), 0,
                        stream, state, w0, f0, out_f, out_w, forcing_hat, nu, nu_stride, drag, dt,
                        stage);
     SPX_LAUNCH_CHECK();
