@@ -6,13 +6,14 @@
 // kernels and write the spectrum to HBM in between.
 //
 // A workgroup owns AP whole arrays (AP n1 n2 ~ 16384 points) and keeps each array's half spectrum
-// in an LDS tile of n1 rows by TS complex values (TS odd and > pad(n2/2), so a row can also hold a
-// padded row transform and the tile's columns fall in distinct banks):
+// in an LDS tile of n1 rows of TS complex values (TS > pad(n2/2), so a row can also hold a padded
+// row transform; the layout that keeps the tile's rows and columns on distinct banks is
+// Fused2d's):
 //
 //   forward  rows: each row of n2 reals is read as n2/2 complex values, transformed in registers
 //            (Stockham stages, exchanges in the tile row itself) and combined in place into its
 //            n2/2 + 1 bins; columns: the first w columns, transformed in place down the tile
-//            (element i of column c at tile[i TS + pad(c)]); store: the kept rows (all n1, or
+//            (element i of column c at tile[row_at(i) + pad(c)]); store: the kept rows (all n1, or
 //            rows 0 .. m1-1 and n1-m1 .. n1-1) of those w columns, contiguous and coalesced.
 //   inverse  the mirror: load the kept rows and columns (zero elsewhere), inverse columns, then per
 //            row the c2r prepare, an inverse n2/2-point transform, and the real row stored.
@@ -53,8 +54,22 @@ struct Fused2d {
     // columns per pass (65 columns of a 128 x 128 half spectrum in two passes, not three);
     // measured 5-9 % faster at 128 x 128, neutral at 64 x 64.
     using PC = Plan<N1, R, (N1 >= 128 ? cmax(16, default_e<N1, R>()) : default_e<N1, R>())>;
-    static constexpr int TS = (pad(M) + 1) | 1;    // tile row stride, odd
-    static constexpr int kTile = N1 * TS;          // complex values per array
+    // Tile layout: row f, column c of array a at tile[a kTile + row_at(f) + pad(c)]. A tile row
+    // holds pad(M) + 1 values (a padded row transform, or the M + 1 bins). One array per
+    // workgroup with rows of 64 complex values or more (128 x 128): row f in tile row pad(f),
+    // tile rows TS = 8 mod 32 apart, and the column passes interleave their columns across each
+    // wave's lanes (col_slot / col_lane), which keeps each half-wave on distinct banks in all but
+    // the first stage's writes (bank conflicts 14 % of column and 20 % of row LDS cycles, against
+    // 50-56 % for odd strides with contiguous column groups). Otherwise rows are TS apart, TS odd.
+    static constexpr int kTsOdd = (pad(M) + 1) | 1;
+    static constexpr int kTsPadded = ((pad(M) + 1 + 23) / 32) * 32 + 8;
+    static constexpr int kRowsPadded = pad(N1 - 1) + 1;
+    static constexpr bool kPadRows = N1 * 2 * M >= 16384 && M >= 64 && N1 >= 16
+                                     && kRowsPadded * kTsPadded * 8 <= BudgetKB * 1024;
+    static constexpr int TS = kPadRows ? kTsPadded : kTsOdd;  // tile row stride
+    static constexpr int kTile = (kPadRows ? kRowsPadded : N1) * TS;  // values per array
+    using ColLay = std::conditional_t<kPadRows, PaddedRows<TS>, Strided<TS>>;
+    __host__ __device__ static constexpr int row_at(int f) { return (kPadRows ? pad(f) : f) * TS; }
     // Arrays per workgroup: about 16384 points, as many as the 80 KB tile budget allows (a
     // power of two, so the row passes still cover the rows exactly).
     static constexpr int kLdsArrays =
@@ -67,8 +82,20 @@ struct Fused2d {
     static constexpr int RPP = NT / PR::L;         // rows per pass
     static constexpr int CPP = NT / PC::L;         // columns per pass
     static constexpr int kMaxLoads = (AP * N1 * (M + 1) + NT - 1) / NT;  // inverse: loads per lane
+    static constexpr int kColsPerWave = 64 / PC::L;
+
+    // Column slot (0 .. CPP-1) and lane of a column pass.
+    __device__ __forceinline__ static int col_slot(int tid)
+    {
+        return kPadRows ? (tid / 64) * kColsPerWave + tid % kColsPerWave : tid / PC::L;
+    }
+    __device__ __forceinline__ static int col_lane(int tid)
+    {
+        return kPadRows ? (tid % 64) / kColsPerWave : tid % PC::L;
+    }
 
     static_assert(PR::L <= 64 && PC::L <= 64, "row and column transforms stay inside a wave");
+    static_assert(!kPadRows || AP == 1, "padded tile rows: one array per workgroup");
     static_assert(kRows % RPP == 0, "row passes cover the rows exactly");
     static_assert(AP * kTile * sizeof(cf32) <= BudgetKB * 1024, "tile exceeds the LDS budget");
     // Flat indices stay below AP N1 (M + 1) and divisors at most N1 (M + 1): FastDiv is exact.
@@ -183,14 +210,14 @@ __device__ __forceinline__ void unpack_dc_nyquist(cf32* tile, int tid)
         const int k1 = e - a * H;
         const int k2 = (F::N1 - k1) & (F::N1 - 1);
         cf32* const t = tile + a * F::kTile;
-        const cf32 p = t[k1 * F::TS];
-        const cf32 q = t[k2 * F::TS];
+        const cf32 p = t[F::row_at(k1)];
+        const cf32 q = t[F::row_at(k2)];
         const cf32 c0{0.5f * (p.re + q.re), 0.5f * (p.im - q.im)};
         const cf32 cm{0.5f * (p.im + q.im), -0.5f * (p.re - q.re)};
-        t[k1 * F::TS] = c0;
-        t[k1 * F::TS + pad(F::M)] = cm;
-        t[k2 * F::TS] = cconj(c0);
-        t[k2 * F::TS + pad(F::M)] = cconj(cm);
+        t[F::row_at(k1)] = c0;
+        t[F::row_at(k1) + pad(F::M)] = cm;
+        t[F::row_at(k2)] = cconj(c0);
+        t[F::row_at(k2) + pad(F::M)] = cconj(cm);
     }
 }
 
@@ -220,14 +247,14 @@ __device__ __forceinline__ void pack_dc_nyquist(cf32* tile, int m1, int tid)
             continue;
         }
         cf32* const t = tile + a * F::kTile;
-        const cf32 a0 = kept1 ? t[k1 * F::TS] : czero();
-        const cf32 b0 = kept2 ? t[k2 * F::TS] : czero();
-        const cf32 am = kept1 ? t[k1 * F::TS + pad(F::M)] : czero();
-        const cf32 bm = kept2 ? t[k2 * F::TS + pad(F::M)] : czero();
+        const cf32 a0 = kept1 ? t[F::row_at(k1)] : czero();
+        const cf32 b0 = kept2 ? t[F::row_at(k2)] : czero();
+        const cf32 am = kept1 ? t[F::row_at(k1) + pad(F::M)] : czero();
+        const cf32 bm = kept2 ? t[F::row_at(k2) + pad(F::M)] : czero();
         const cf32 h0{0.5f * (a0.re + b0.re), 0.5f * (a0.im - b0.im)};
         const cf32 hm{0.5f * (am.re + bm.re), 0.5f * (am.im - bm.im)};
-        t[k1 * F::TS] = cf32{h0.re - hm.im, h0.im + hm.re};
-        t[k2 * F::TS] = cf32{h0.re + hm.im, hm.re - h0.im};
+        t[F::row_at(k1)] = cf32{h0.re - hm.im, h0.im + hm.re};
+        t[F::row_at(k2)] = cf32{h0.re + hm.im, hm.re - h0.im};
     }
 }
 
@@ -240,7 +267,7 @@ __device__ __forceinline__ bool packed_kept(int i, int m1, bool packed_column)
 
 // Whole half spectra (m1 = 0, w = M + 1), HBM -> tile, for rows of M >= 32 complex values: row
 // by row, with no index division. Wave v owns rows v RPW .. v RPW + RPW-1 of the workgroup's
-// arrays (arrays are contiguous in the tile, kTile = N1 TS, and in HBM); lane l holds column
+// arrays (arrays are contiguous in the tile, kTile apart, and in HBM); lane l holds column
 // c = l mod M (plus 64 j, j < CW, when M = 128) of row l / M of each step, so a step's tile and
 // HBM addresses are the lane's own plus compile-time offsets. Column M (the Nyquist bins) takes
 // one more step, lane l < RPW holding row l's. (The same order for the forward's stores measured
@@ -276,17 +303,17 @@ struct FullRows {
             constexpr int i = decltype(ii)::value;
             static_for<0, CW>([&](auto jj) {
                 constexpr int j = decltype(jj)::value;
-                tile[(row + i * RW) * F::TS + pad(col + 64 * j)] = val[i][j];
+                tile[F::row_at(row + i * RW) + pad(col + 64 * j)] = val[i][j];
             });
         });
         if (tid % 64 < RPW) {
-            tile[nrow * F::TS + pad(F::M)] = ny;
+            tile[F::row_at(nrow) + pad(F::M)] = ny;
         }
     }
 };
 
 // Whole half spectra, tile -> HBM (dst: the workgroup's first array), flat: element e = row W + c
-// (W = M + 1, rows counted across the workgroup's arrays) goes to dst[e] from tile[row TS +
+// (W = M + 1, rows counted across the workgroup's arrays) goes to dst[e] from tile[row_at(row) +
 // pad(c)], lane t taking e = t + k NT. (row, c) advances by a compile-time step from one k to
 // the next, so no element needs a division; stores are full 128-byte lines.
 template <class F>
@@ -304,7 +331,7 @@ __device__ __forceinline__ void store_full(const cf32* tile, cf32* dst, int coun
         cf32 val[n];
         static_for<0, n>([&](auto ki) {
             constexpr int k = decltype(ki)::value;
-            val[k] = tile[cmin(row, F::kRows - 1) * F::TS + pad(c)];
+            val[k] = tile[F::row_at(cmin(row, F::kRows - 1)) + pad(c)];
             c += F::NT % W;
             row += F::NT / W;
             if (c >= W) {
@@ -371,7 +398,7 @@ __global__ void __launch_bounds__(F::NT)
     static_for<0, kPasses>([&](auto pi) {
         constexpr int p = decltype(pi)::value;
         const int row = p * F::RPP + tid / PR::L;
-        cf32* const s = tile + (row / F::N1) * F::kTile + (row % F::N1) * F::TS;
+        cf32* const s = tile + (row / F::N1) * F::kTile + F::row_at(row % F::N1);
         run_stages<PR, 0, false, F::kTable>(v[p], s, lane, table);
         lds_sync<true>();
         final_write<PR>(s, v[p], lane);
@@ -385,17 +412,17 @@ __global__ void __launch_bounds__(F::NT)
     const int total_cols = F::AP * ncols;
 #pragma unroll 1
     for (int c0 = 0; c0 < total_cols; c0 += F::CPP) {
-        const int cg = c0 + tid / PC::L;
-        const int lane = tid % PC::L;
+        const int cg = c0 + F::col_slot(tid);
+        const int lane = F::col_lane(tid);
         if (cg < total_cols) {
             const int a = pack ? cg / F::M : static_cast<int>(wdiv.div(static_cast<unsigned>(cg)));
             const int c = cg - a * ncols;
             cf32* const s = tile + a * F::kTile + pad(c);
             cf32 v[PC::E];
-            stage_read<PC, 0, Strided<F::TS>>(s, v, lane);
-            run_stages<PC, 0, false, F::kTable, Strided<F::TS>>(v, s, lane, table);
+            stage_read<PC, 0, typename F::ColLay>(s, v, lane);
+            run_stages<PC, 0, false, F::kTable, typename F::ColLay>(v, s, lane, table);
             lds_sync<true>();
-            final_write<PC, Strided<F::TS>>(s, v, lane);
+            final_write<PC, typename F::ColLay>(s, v, lane);
         }
     }
     __syncthreads();
@@ -427,7 +454,7 @@ __global__ void __launch_bounds__(F::NT)
             const int a = F::AP == 1 ? 0 : static_cast<int>(odiv.div(static_cast<unsigned>(e)));
             const int r = e - a * per_array;
             const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(r)));
-            val[k] = tile[a * F::kTile + F::row_of(f, m1) * F::TS + pad(r - f * w)];
+            val[k] = tile[a * F::kTile + F::row_at(F::row_of(f, m1)) + pad(r - f * w)];
         }
 #pragma unroll
         for (int k = 0; k < kStoreChunk; ++k) {
@@ -491,7 +518,7 @@ __global__ void __launch_bounds__(F::NT)
                 const int rem = e - a * per_array;
                 const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(rem)));
                 const int c = rem - f * w;
-                tile[a * F::kTile + F::row_of(f, m1) * F::TS + pad(c)] = val[k];
+                tile[a * F::kTile + F::row_at(F::row_of(f, m1)) + pad(c)] = val[k];
             }
         }
     }
@@ -507,15 +534,15 @@ __global__ void __launch_bounds__(F::NT)
     constexpr int R0 = PC::template radix<0>();
 #pragma unroll 1
     for (int c0 = 0; c0 < total_cols; c0 += F::CPP) {
-        const int cg = c0 + tid / PC::L;
-        const int lane = tid % PC::L;
+        const int cg = c0 + F::col_slot(tid);
+        const int lane = F::col_lane(tid);
         if (cg < total_cols) {
             const int a = pack ? cg / F::M : static_cast<int>(wdiv.div(static_cast<unsigned>(cg)));
             const int c = cg - a * ncols;
             cf32* const s = tile + a * F::kTile + pad(c);
             cf32 v[PC::E];
             if (m1 == 0) {
-                stage_read<PC, 0, Strided<F::TS>>(s, v, lane);
+                stage_read<PC, 0, typename F::ColLay>(s, v, lane);
             } else {
 #pragma unroll
                 for (int b = 0; b < PC::E / R0; ++b) {
@@ -523,13 +550,13 @@ __global__ void __launch_bounds__(F::NT)
                     for (int r = 0; r < R0; ++r) {
                         const int i = input_index<PC, 0>(lane, b, r);
                         const bool kept = packed_kept<F>(i, m1, pack && c == 0);
-                        v[b * R0 + r] = kept ? s[i * F::TS] : czero();
+                        v[b * R0 + r] = kept ? s[F::ColLay::at(i)] : czero();
                     }
                 }
             }
-            run_stages<PC, 0, true, F::kTable, Strided<F::TS>>(v, s, lane, table);
+            run_stages<PC, 0, true, F::kTable, typename F::ColLay>(v, s, lane, table);
             lds_sync<true>();
-            final_write<PC, Strided<F::TS>>(s, v, lane);
+            final_write<PC, typename F::ColLay>(s, v, lane);
         }
     }
     __syncthreads();
@@ -543,7 +570,7 @@ __global__ void __launch_bounds__(F::NT)
         const int row = p * F::RPP + tid / PR::L;
         const int lane = tid % PR::L;
         const int a = row / F::N1;
-        cf32* const s = tile + a * F::kTile + (row % F::N1) * F::TS;
+        cf32* const s = tile + a * F::kTile + F::row_at(row % F::N1);
         prepare_row<F::M, PR::L>(s, lane, w, pack, half);
         lds_sync<true>();
         cf32 v[PR::E];
@@ -577,7 +604,7 @@ __global__ void __launch_bounds__(F::NT)
                 const int aw = rw / F::N1;
                 if (aw < count) {
                     st_stream(z + (first * F::N1 + rw) * F::M + i,
-                              tile[aw * F::kTile + (rw % F::N1) * F::TS + pad(i)]);
+                              tile[aw * F::kTile + F::row_at(rw % F::N1) + pad(i)]);
                 }
             }
         }
@@ -622,7 +649,7 @@ __global__ void __launch_bounds__(F::NT)
             const int a = e / kPerArray;
             const int r = e - a * kPerArray;
             const int f = r / F::M;
-            tile[a * F::kTile + f * F::TS + pad(r - f * F::M)] = val[k];
+            tile[a * F::kTile + F::row_at(f) + pad(r - f * F::M)] = val[k];
         }
         __syncthreads();
     }
@@ -631,7 +658,7 @@ __global__ void __launch_bounds__(F::NT)
         const int row = p * F::RPP + tid / PR::L;  // row of the workgroup's arrays
         const int lane = tid % PR::L;
         const int a = row / F::N1;
-        cf32* const s = tile + a * F::kTile + (row % F::N1) * F::TS;
+        cf32* const s = tile + a * F::kTile + F::row_at(row % F::N1);
         cf32 v[PR::E];
         if constexpr (kStaged) {
             stage_read<PR, 0>(s, v, lane);
@@ -654,17 +681,17 @@ __global__ void __launch_bounds__(F::NT)
 
 #pragma unroll 1
     for (int c0 = 0; c0 < F::AP * F::M; c0 += F::CPP) {
-        const int cg = c0 + tid / PC::L;
-        const int lane = tid % PC::L;
+        const int cg = c0 + F::col_slot(tid);
+        const int lane = F::col_lane(tid);
         if (cg < F::AP * F::M) {
             const int a = cg / F::M;
             const int c = cg - a * F::M;
             cf32* const s = tile + a * F::kTile + pad(c);
             cf32 v[PC::E];
-            stage_read<PC, 0, Strided<F::TS>>(s, v, lane);
-            run_stages<PC, 0, Inv, F::kTable, Strided<F::TS>>(v, s, lane, table);
+            stage_read<PC, 0, typename F::ColLay>(s, v, lane);
+            run_stages<PC, 0, Inv, F::kTable, typename F::ColLay>(v, s, lane, table);
             lds_sync<true>();
-            final_write<PC, Strided<F::TS>>(s, v, lane);
+            final_write<PC, typename F::ColLay>(s, v, lane);
         }
     }
     __syncthreads();
@@ -682,7 +709,7 @@ __global__ void __launch_bounds__(F::NT)
                 const int a = e / kPerArray;
                 const int r = e - a * kPerArray;
                 const int f = r / F::M;
-                val[k] = tile[a * F::kTile + f * F::TS + pad(r - f * F::M)];
+                val[k] = tile[a * F::kTile + F::row_at(f) + pad(r - f * F::M)];
             }
         }
 #pragma unroll

@@ -90,12 +90,6 @@ struct NsPairPlan {
     static_assert(kLds * sizeof(cf32) <= 160 * 1024, "LDS budget");
 };
 
-// A column of the tile: element i at tile row pad(i).
-template <int Stride>
-struct PaddedRows {
-    __host__ __device__ static constexpr int at(int i) { return pad(i) * Stride; }
-};
-
 // Column slot and lane of a column phase: the wave's lanes interleave its kPerWave columns.
 template <class NP>
 __device__ __forceinline__ int column_slot(int tid)

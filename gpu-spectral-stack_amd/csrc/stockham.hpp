@@ -398,8 +398,9 @@ __device__ __forceinline__ void lds_sync()
 // --- stage pieces ---------------------------------------------------------------------------
 //
 // A transform's values sit in LDS in one of two layouts: element i at s[Lay::at(i)].
-//   Padded       one complex of padding after every 16 (a transform stored as a row)
-//   Strided<ST>  every ST values (a column of a row-major tile whose rows are ST long)
+//   Padded         one complex of padding after every 16 (a transform stored as a row)
+//   Strided<ST>    every ST values (a column of a row-major tile whose rows are ST long)
+//   PaddedRows<ST> a column of a tile with a spare row after every 16 rows
 // LDS addresses are a per-lane base plus a compile-time offset. For Strided that is linearity;
 // for Padded, pad(a + c) = pad(a) + pad(c) whenever the low four bits of a and c add without a
 // carry, and for every access pattern below that holds for all lanes (power-of-two strides,
@@ -413,6 +414,13 @@ struct Padded {
 template <int Stride>
 struct Strided {
     __host__ __device__ static constexpr int at(int i) { return i * Stride; }
+};
+
+// A column of a tile whose element i sits in tile row pad(i) (one spare row after every 16),
+// tile rows Stride apart.
+template <int Stride>
+struct PaddedRows {
+    __host__ __device__ static constexpr int at(int i) { return pad(i) * Stride; }
 };
 
 template <class P, class Lay>
