@@ -7,7 +7,7 @@
 // The general single-pass kernels keep a whole half spectrum in LDS (at 128 x 128, 70 KB: two
 // arrays per CU), although only w columns outlive the row pass. Here the row transforms exchange
 // through a scratch of one pass's rows, and only the w kept bins of each row go to a narrow
-// column tile (N1 rows by TC >= w values): at 128 x 128 with w <= 16, 35 KB, so four arrays share
+// column tile (N1 rows by TC >= w values): at 128 x 128 with w <= 16, 40 KB, so four arrays share
 // a CU and more of the HBM traffic overlaps the transforms.
 //
 //   forward  every row pass's loads first, then per pass: row transform (exchanges in the
@@ -34,10 +34,18 @@ struct Modes2d {
     static constexpr int NT = 256;
     static constexpr int RPP = NT / PR::L;        // rows per pass
     static constexpr int kPasses = N1 / RPP;
-    static constexpr int TR = (pad(M) + 1) | 1;   // scratch row stride
-    static constexpr int TC = WMax | 1;           // tile row stride, odd
+    // LDS layouts (64 banks of 4 bytes, 8-byte accesses served a half-wave at a time). Scratch
+    // rows of 64 values sit 72 apart (8 mod 32), other lengths an odd stride. Tile (n1 >= 64,
+    // rows of 64 values or more): row f in tile row pad(f), tile rows TC = 4 mod 8 apart. Bank
+    // conflicts in the 128 x 128 kernels' row and column passes: 20 % and 14 % of LDS cycles,
+    // against 56 % and 50 % with odd strides.
+    static constexpr int TR = M == 64 ? 72 : (pad(M) + 1) | 1;  // scratch row stride
+    static constexpr bool kPadRows = N1 >= 64 && M >= 64;
+    static constexpr int TC = kPadRows ? (WMax + 3) / 8 * 8 + 4 : WMax | 1;  // tile row stride
     static constexpr int kScratch = RPP * TR;
-    static constexpr int kTile = N1 * TC;
+    static constexpr int kTile = (kPadRows ? pad(N1 - 1) + 1 : N1) * TC;
+    using ColLay = std::conditional_t<kPadRows, PaddedRows<TC>, Strided<TC>>;
+    __host__ __device__ static constexpr int tile_row(int f) { return (kPadRows ? pad(f) : f) * TC; }
     static constexpr int kMaxIo = (N1 * WMax + NT - 1) / NT;  // flat modes per lane, at most
 
     static_assert(kPasses >= 1 && N1 % RPP == 0, "row passes cover the rows exactly");
@@ -94,7 +102,7 @@ __global__ void __launch_bounds__(F::NT)
         lds_sync<true>();
         final_write<PR>(s, v[p], lane);
         lds_sync<true>();
-        cf32* const trow = tile + (p * F::RPP + prow) * F::TC;
+        cf32* const trow = tile + F::tile_row(p * F::RPP + prow);
         static_for<0, F::WMax / PR::L + 1>([&](auto ji) {
             constexpr int j = decltype(ji)::value;
             const int k = lane + j * PR::L;
@@ -120,10 +128,10 @@ __global__ void __launch_bounds__(F::NT)
         if (c < w) {
             cf32* const col = tile + c;
             cf32 u[PC::E];
-            stage_read<PC, 0, Strided<F::TC>>(col, u, clane);
-            run_stages<PC, 0, false, F::kTable, Strided<F::TC>>(u, col, clane, table);
+            stage_read<PC, 0, typename F::ColLay>(col, u, clane);
+            run_stages<PC, 0, false, F::kTable, typename F::ColLay>(u, col, clane, table);
             lds_sync<true>();
-            final_write<PC, Strided<F::TC>>(col, u, clane);
+            final_write<PC, typename F::ColLay>(col, u, clane);
         }
     }
     __syncthreads();
@@ -133,7 +141,7 @@ __global__ void __launch_bounds__(F::NT)
     cf32* const dst = y + array * total;
     for (int e = tid; e < total; e += F::NT) {
         const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(e)));
-        st_stream(dst + e, tile[F::row_of(f, m1) * F::TC + (e - f * w)]);
+        st_stream(dst + e, tile[F::tile_row(F::row_of(f, m1)) + (e - f * w)]);
     }
 }
 
@@ -166,7 +174,7 @@ __global__ void __launch_bounds__(F::NT)
         if (k * F::NT < total) {
             const int e = cmin(tid + k * F::NT, total - 1);
             const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(e)));
-            tile[F::row_of(f, m1) * F::TC + (e - f * w)] = val[k];
+            tile[F::tile_row(F::row_of(f, m1)) + (e - f * w)] = val[k];
         }
     }
     __syncthreads();
@@ -187,12 +195,13 @@ __global__ void __launch_bounds__(F::NT)
 #pragma unroll
                 for (int r = 0; r < RC; ++r) {
                     const int i = input_index<PC, 0>(clane, b, r);
-                    u[b * RC + r] = (i < m1 || i >= F::N1 - m1) ? col[i * F::TC] : czero();
+                    u[b * RC + r] =
+                        (i < m1 || i >= F::N1 - m1) ? col[F::ColLay::at(i)] : czero();
                 }
             }
-            run_stages<PC, 0, true, F::kTable, Strided<F::TC>>(u, col, clane, table);
+            run_stages<PC, 0, true, F::kTable, typename F::ColLay>(u, col, clane, table);
             lds_sync<true>();
-            final_write<PC, Strided<F::TC>>(col, u, clane);
+            final_write<PC, typename F::ColLay>(col, u, clane);
         }
     }
     __syncthreads();
@@ -213,7 +222,7 @@ __global__ void __launch_bounds__(F::NT)
 #pragma unroll 1
     for (int p = 0; p < F::kPasses; ++p) {
         const int row = p * F::RPP + prow;
-        const cf32* const trow = tile + row * F::TC;
+        const cf32* const trow = tile + F::tile_row(row);
         cf32 v[PR::E];
         static_for<0, PR::E>([&](auto ei) {
             constexpr int e = decltype(ei)::value;
