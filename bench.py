@@ -28,7 +28,7 @@ extra        secondary rows of the metric, each with rocFFT (torch.fft) on the s
 Launches rotate over buffer sets totalling well over twice the 256 MB Infinity Cache, so a
 launch cannot read what the previous one left in the cache.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--impl NAME]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--impl NAME] [--no-extra | --extra LIST]
 """
 
 from __future__ import annotations
@@ -52,6 +52,12 @@ PEAK_GBPS = 8000.0
 SETS = 4  # 4 x (x, y, z) x 128 MiB = 1.5 GiB in rotation
 
 
+# Secondary row groups, in the order they run: C-ABI timings of the 2D and pruned configurations,
+# the C2 size sweep, the torch-operator rows (C2, C3, C4, large C2C), the Navier-Stokes solvers
+# (C5) and the radio callers.
+EXTRA_GROUPS = ("capi", "sweep", "secondary", "ns", "radio")
+
+
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -61,7 +67,16 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time spent on the numpy baseline sample")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary rows")
-    return ap.parse_args(argv)
+    ap.add_argument("--extra", default=",".join(EXTRA_GROUPS),
+                    help="comma-separated groups of secondary rows to run (default: all of "
+                         + ", ".join(EXTRA_GROUPS) + ")")
+    args = ap.parse_args(argv)
+    groups = [] if args.no_extra else [g for g in args.extra.split(",") if g]
+    unknown = sorted(set(groups) - set(EXTRA_GROUPS))
+    if unknown:
+        ap.error(f"unknown --extra group(s) {', '.join(unknown)}")
+    args.extra = groups
+    return args
 
 
 def load_capi():
@@ -251,15 +266,20 @@ def main(argv=None) -> int:
              "fwd_gbps": round(achieved, 1), "wall_s_timed": round(wall_s, 3)}
     extra["copy_gbps"] = round(copy_gbps, 1)
     extra["c1_pct_of_copy"] = round(100 * value / copy_gbps, 1)
-    if not args.no_extra:
+    if args.extra:
         # Every row of this stack first; rocFFT's (through torch.fft) after all of them: rocFFT's
         # kernels on random data slowed this stack's launches that followed them by 5-12 %.
         later = []
-        extra.update(capi_rows(lib, impl, dev, stream))
-        extra.update(sweep_rows(lib, impl, dev, stream, later))
-        extra.update(secondary_rows(args.impl, dev, later))
-        extra.update(navier_stokes_rows(args.impl, dev, later))
-        extra.update(radio_rows(args.impl, dev, later))
+        groups = {
+            "capi": lambda: capi_rows(lib, impl, dev, stream),
+            "sweep": lambda: sweep_rows(lib, impl, dev, stream, later),
+            "secondary": lambda: secondary_rows(args.impl, dev, later),
+            "ns": lambda: navier_stokes_rows(args.impl, dev, later),
+            "radio": lambda: radio_rows(args.impl, dev, later),
+        }
+        for name in EXTRA_GROUPS:
+            if name in args.extra:
+                extra.update(groups[name]())
         for rocfft_rows in later:
             extra.update(rocfft_rows())
 

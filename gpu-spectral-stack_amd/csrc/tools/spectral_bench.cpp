@@ -48,7 +48,7 @@ constexpr double kUnstableSpread = 0.05;  // max / min - 1 above this gets a war
 const char* const kUsage =
     "usage: spectral_bench [options]\n"
     "  --op NAME       all (default), fft_c2c, fft_r2c, fft_c2r, fft2_c2c, fft2_r2c,\n"
-    "                  fft2_c2r, rfft2_modes, irfft2_modes, or scale\n"
+    "                  fft2_c2r, rfft2_modes, irfft2_modes, scale, or ns_step\n"
     "  --impl NAME     all (default), rocfft, ours (the scale kernel), or one of our FFTs\n"
     "  --sizes LIST    comma-separated transform sizes (default: 2,4,...,4096)\n"
     "  --total N       points per row; batch = total / n (default: 16777216)\n"
@@ -168,7 +168,7 @@ Options parse_options(int argc, char** argv)
     }
     static const char* const ops[] = {"all",      "fft_c2c",  "fft_r2c",     "fft_c2r",
                                       "fft2_c2c", "fft2_r2c", "fft2_c2r",    "rfft2_modes",
-                                      "irfft2_modes", "scale"};
+                                      "irfft2_modes", "scale",    "ns_step"};
     if (std::none_of(std::begin(ops), std::end(ops), [&](const char* s) { return o.op == s; })) {
         throw std::invalid_argument("unknown --op " + o.op + "\n" + kUsage);
     }
@@ -645,6 +645,55 @@ void bench_modes(const Options& o, const std::string& op, Buffers& b, hipStream_
     }
 }
 
+// One IMEX step of the fused Navier-Stokes solver, the predictor and the corrector launch of
+// spx_ns_stage, on batch fields of n x n grids in the pruned layout (m = n/3 + 1 kept modes per
+// axis; n with a kernel only). Work per step: the nominal flops of the transforms the composed
+// solver runs (per stage four inverse and one forward real 2D transform, 2.5 n^2 log2 n^2 each)
+// and the HBM bytes of the mode arrays (stage 0 reads the state and writes the tendency and the
+// predictor; stage 1 reads the predictor, the state and the tendency and writes the new state;
+// the forcing modes once per stage).
+void bench_ns(const Options& o, Buffers& b, hipStream_t s, std::ostream& os, bool progress)
+{
+    for (const Case& c : cases(o, 2)) {
+        if (c.n > 4096 || spx_ns_supports(static_cast<int>(c.n)) != 1) {
+            continue;
+        }
+        const int n = static_cast<int>(c.n);
+        const int batch = static_cast<int>(c.batch);
+        const std::size_t m = static_cast<std::size_t>(n / 3 + 1);
+        const std::size_t field = 2 * m * m * 8;  // bytes of one field's modes
+        if (3 * field * c.batch > b.bytes) {
+            continue;  // the output buffer holds the tendency, the predictor and the new state
+        }
+        Scratch forcing(field);
+        hip_check(hipMemset(forcing.p, 0, field), "hipMemset");
+        Scratch nu(static_cast<std::size_t>(batch) * sizeof(float));
+        const std::vector<float> nu_host(static_cast<std::size_t>(batch), 2e-3f);
+        hip_check(hipMemcpy(nu.p, nu_host.data(), nu_host.size() * sizeof(float),
+                            hipMemcpyHostToDevice),
+                  "hipMemcpy");
+        const double points = static_cast<double>(n) * n;
+        const Work w{2.0 * 5.0 * 2.5 * points * std::log2(points) * c.batch,
+                     (7.0 * c.batch + 2.0) * static_cast<double>(field)};
+        const auto* viscosity = static_cast<const float*>(nu.p);
+        const Timing t = time_launches(
+            [&](int k, hipStream_t st) {
+                char* const y = static_cast<char*>(b.y[k]);
+                void* const f = y;
+                void* const p = y + field * c.batch;
+                void* const out = y + 2 * field * c.batch;
+                spx_check(spx_ns_stage(b.x[k], nullptr, nullptr, f, p, forcing.p, viscosity, 1,
+                                       0.1f, 2.5e-3f, n, batch, 0, st),
+                          "spx_ns_stage");
+                spx_check(spx_ns_stage(p, b.x[k], f, nullptr, out, forcing.p, viscosity, 1,
+                                       0.1f, 2.5e-3f, n, batch, 1, st),
+                          "spx_ns_stage");
+            },
+            s, o);
+        write_row(os, "ns_step", "ours", c.n, c.batch, t, w, progress);
+    }
+}
+
 void bench_scale(const Options& o, Buffers& b, hipStream_t s, std::ostream& os, bool progress)
 {
     const auto n = static_cast<std::size_t>(o.total);
@@ -700,6 +749,9 @@ int main(int argc, char** argv)
         }
         if (want("scale") && o.wants("ours")) {
             bench_scale(o, buffers, stream, os, progress);
+        }
+        if (want("ns_step") && o.wants("ours")) {
+            bench_ns(o, buffers, stream, os, progress);
         }
         hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
         hip_check(hipStreamDestroy(stream), "hipStreamDestroy");

@@ -91,3 +91,13 @@ def test_cpu_baseline_reports_its_sample_and_the_wider_rows():
     assert "on 1 host thread" in cb["sample"]
     if "scipy_all_cores_gbps" in cb:
         assert cb["scipy_all_cores_gbps"] > 0 and cb["scipy_threads"] >= 1
+
+
+def test_bench_row_groups_select_and_reject():
+    import bench
+
+    assert bench.parse_args([]).extra == list(bench.EXTRA_GROUPS)
+    assert bench.parse_args(["--no-extra"]).extra == []
+    assert bench.parse_args(["--extra", "ns,capi"]).extra == ["ns", "capi"]
+    with pytest.raises(SystemExit):
+        bench.parse_args(["--extra", "ns,bogus"])

@@ -399,9 +399,12 @@ def test_mode_gather_and_scatter_edges(lib, rng, n1, w, m1, m2):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize(("rows", "cols", "batch"), [(1, 1, 3), (64, 64, 2), (65, 63, 3),
-                                                     (1024, 16384, 1), (3, 200, 7), (513, 1, 2)])
+                                                     (1024, 16384, 1), (3, 200, 7), (513, 1, 2),
+                                                     (4, 3, 4096), (31, 40, 5), (1000, 20, 2),
+                                                     (32, 32, 3)])
 def test_transpose_is_exact(lib, rng, rows, cols, batch):
-    # Partial tiles on both axes, a single column or row, and the four-step's 1024 x 16384.
+    # Partial tiles on both axes, a single column or row, and the four-step's 1024 x 16384; arrays
+    # with fewer than 32 rows or columns take the flat path (4 x 3: a 4 x 4 real transform's).
     x = (rng.standard_normal((batch, rows, cols)) + 1j * rng.standard_normal((batch, rows, cols)))
     xd = torch.from_numpy(x.astype(np.complex64)).cuda()
     yd = torch.empty(batch, cols, rows, dtype=torch.complex64, device="cuda")
