@@ -59,6 +59,7 @@ CASES_2D = [
     (64, 32, 12, 12),
     (32, 128, 4, 20),
     (256, 256, 16, 16),
+    (1024, 16, 100, 5),
     (4096, 2, 2, 2),
     (2, 8192, 1, 64),
     (128, 128, 16, 16),
