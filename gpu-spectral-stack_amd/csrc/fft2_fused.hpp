@@ -43,7 +43,7 @@ struct FastDiv {
     __device__ __forceinline__ unsigned div(unsigned x) const { return __umulhi(x << 1, m); }
 };
 
-template <int N1_, int M_, int R, bool Table, int BudgetKB = 80>
+template <int N1_, int M_, int R, bool Table, int BudgetKB = 80, int Threads = 512>
 struct Fused2d {
     static constexpr int N1 = N1_;                 // rows (column transform length)
     static constexpr int M = M_;                   // complex values per real row (n2 / 2)
@@ -76,7 +76,7 @@ struct Fused2d {
         BudgetKB * 1024 / (kTile * static_cast<int>(sizeof(cf32)));
     static constexpr int AP = cmin(cmax(1, 16384 / (N1 * N2)),
                                    1 << (31 - __builtin_clz(cmax(1, kLdsArrays))));
-    static constexpr int NT = 512;                 // lanes per workgroup
+    static constexpr int NT = Threads;             // lanes per workgroup
     static constexpr int NW = NT / 64;
     static constexpr int kRows = AP * N1;
     static constexpr int RPP = NT / PR::L;         // rows per pass
