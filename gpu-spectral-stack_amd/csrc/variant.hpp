@@ -170,7 +170,10 @@ void dispatch_strided_columns(int n, const StridedIo& io, long long batch, hipSt
                                   Table>(io, batch, stream);
         break;
     case 1024:
-        launch_columns_persistent<Plan<1024, R, 16, 512>, Inv, Table, 32>(io, batch, stream);
+        // Radix 16 in the radix-8 variants (two exchanges instead of three): the 2^20-point
+        // C2C over 2^24 points 115.6 -> 112.0 us in interleaved runs.
+        launch_columns_persistent<Plan<1024, (R == 8 ? 16 : R), 16, 512>, Inv, Table, 32>(
+            io, batch, stream);
         break;
     default:
         dispatch_columns<R, Inv, Table>(n, io, batch, stream);
