@@ -184,11 +184,13 @@ __device__ __forceinline__ void pair_row_inverse(cf32* row, cf32 (&v)[NP::PX::E]
 
 template <class NP>
 __global__ void __launch_bounds__(NP::NT)
-    ns_stage_kernel(const cf32* __restrict__ state, const cf32* __restrict__ w0,
-                   const cf32* __restrict__ f0, cf32* __restrict__ out_f,
-                   cf32* __restrict__ out_w, const cf32* __restrict__ forcing_hat,
-                   const float* __restrict__ nu, int nu_stride, float drag, float dt, int stage)
+    ns_stage_kernel(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32* out_w,
+                    const cf32* __restrict__ forcing_hat, const float* __restrict__ nu,
+                    int nu_stride, float drag, float dt, int stage)
 {
+    // out_f and out_w may overwrite state, w0 or f0 (the C ABI allows it): every read of the
+    // state happens before the barrier that ends the transforms, and the epilogue loads all the
+    // values a lane updates before it stores any, so those pointers are not restrict.
     using PX = typename NP::PX;
     __shared__ cf32 T[NP::kLds];
     const int tid = threadIdx.x;
@@ -253,27 +255,44 @@ __global__ void __launch_bounds__(NP::NT)
     }
     __syncthreads();
 
-    // Epilogue on the kept modes.
+    // Epilogue on the kept modes: every global value a lane reads is loaded before its stores.
+    constexpr int kIters = (NP::kW + NP::NT - 1) / NP::NT;
     const float nu_f = nu[field * nu_stride];
     const float kmax = static_cast<float>(NP::N) / 3.0f;
-    for (int e = tid; e < NP::kW; e += NP::NT) {
-        const int r = e / NP::m;
-        const int c = e - r * NP::m;
-        const float ky = ky_of_mode_row<NP>(r);
-        const float kx = static_cast<float>(c);
-        const int i = r < NP::m ? r : r - 2 * NP::m + NP::N;
-        const bool kept = fabsf(kx) <= kmax && fabsf(ky) <= kmax;
-        const cf32 nlh = kept ? T[pad(i) * NP::RS + c] : czero();
-        const cf32 F = csub(forcing_hat[e], nlh);
-        const float linear = -nu_f * (kx * kx + ky * ky) - drag;
-        const float ex = 1.0f + 0.5f * dt * linear;
-        const float im = 1.0f / (1.0f - 0.5f * dt * linear);
-        if (stage == 0) {
-            out_f[base + e] = F;
-            out_w[base + e] = cscale(cadd(cscale(w[e], ex), cscale(F, dt)), im);
-        } else {
-            const cf32 sum = cadd(f0[base + e], F);
-            out_w[base + e] = cscale(cadd(cscale(w0[base + e], ex), cscale(sum, 0.5f * dt)), im);
+    cf32 fh[kIters];
+    cf32 wv[kIters];
+    cf32 fv[kIters];
+#pragma unroll
+    for (int q = 0; q < kIters; ++q) {
+        const int e = tid + q * NP::NT;
+        if (e < NP::kW) {
+            fh[q] = forcing_hat[e];
+            wv[q] = stage == 0 ? w[e] : w0[base + e];
+            fv[q] = stage == 0 ? czero() : f0[base + e];
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < kIters; ++q) {
+        const int e = tid + q * NP::NT;
+        if (e < NP::kW) {
+            const int r = e / NP::m;
+            const int c = e - r * NP::m;
+            const float ky = ky_of_mode_row<NP>(r);
+            const float kx = static_cast<float>(c);
+            const int i = r < NP::m ? r : r - 2 * NP::m + NP::N;
+            const bool kept = fabsf(kx) <= kmax && fabsf(ky) <= kmax;
+            const cf32 nlh = kept ? T[pad(i) * NP::RS + c] : czero();
+            const cf32 F = csub(fh[q], nlh);
+            const float linear = -nu_f * (kx * kx + ky * ky) - drag;
+            const float ex = 1.0f + 0.5f * dt * linear;
+            const float im = 1.0f / (1.0f - 0.5f * dt * linear);
+            if (stage == 0) {
+                out_f[base + e] = F;
+                out_w[base + e] = cscale(cadd(cscale(wv[q], ex), cscale(F, dt)), im);
+            } else {
+                const cf32 sum = cadd(fv[q], F);
+                out_w[base + e] = cscale(cadd(cscale(wv[q], ex), cscale(sum, 0.5f * dt)), im);
+            }
         }
     }
 }

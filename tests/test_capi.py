@@ -261,6 +261,39 @@ def test_direct_radio_and_navier_stokes_calls(lib, rng):
     assert torch.equal(f0, ref_f0) and torch.equal(pred, ref_pred)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [64, 128])
+def test_ns_stage_may_write_over_its_inputs(lib, rng, n):
+    # Stage 0 with the predictor written over the state, stage 1 with the new state written over
+    # w0 and then over the predictor: each must equal the same stage into fresh outputs.
+    from spectral.flow import Flow
+    from spectral.flow.gpu import GpuSolver
+
+    solver = GpuSolver(n, Flow(viscosity=np.array([1e-3, 4e-3])), 2.5e-3, pruned=True)
+    w = solver.to_spectral(torch.from_numpy(rng.standard_normal((2, n, n))).float().cuda())
+    args = (_ptr(solver.forcing_hat), ctypes.c_void_p(solver.nu.data_ptr()), 1,
+            ctypes.c_float(0.1), ctypes.c_float(2.5e-3), n, 2)
+    f0 = torch.empty_like(w)
+    pred = torch.empty_like(w)
+    assert lib.spx_ns_stage(_ptr(w), None, None, _ptr(f0), _ptr(pred), *args, 0, None) == SPX_OK
+    new = torch.empty_like(w)
+    assert lib.spx_ns_stage(_ptr(pred), _ptr(w), _ptr(f0), None, _ptr(new), *args, 1,
+                            None) == SPX_OK
+
+    over = w.clone()
+    f0_over = torch.empty_like(w)
+    assert lib.spx_ns_stage(_ptr(over), None, None, _ptr(f0_over), _ptr(over), *args, 0,
+                            None) == SPX_OK
+    w0 = w.clone()
+    assert lib.spx_ns_stage(_ptr(pred), _ptr(w0), _ptr(f0), None, _ptr(w0), *args, 1,
+                            None) == SPX_OK
+    p = pred.clone()
+    assert lib.spx_ns_stage(_ptr(p), _ptr(w), _ptr(f0), None, _ptr(p), *args, 1, None) == SPX_OK
+    torch.cuda.synchronize()
+    assert torch.equal(over, pred) and torch.equal(f0_over, f0)
+    assert torch.equal(w0, new) and torch.equal(p, new)
+
+
 def _fft_columns(x: np.ndarray, inverse: bool) -> np.ndarray:
     from oracle import reference as ref
 
