@@ -151,8 +151,8 @@ void launch_columns_persistent(const StridedIo& io, long long batch, hipStream_t
     SPX_LAUNCH_CHECK();
 }
 
-// Strided columns of 256, 512 and 1024 points run persistent (columns_kernel); other lengths keep
-// one tile per workgroup (persistent measured 2-3 points faster at 128). The 1024-point tiles hold
+// Strided columns of 256, 512 and 1024 points, and of 64 and 128 points in wide matrices, run
+// persistent (columns_kernel); other lengths keep one tile per workgroup. The 1024-point tiles hold
 // 8 columns of 16 values per lane, one wave per column (workgroups of 512 lanes), in XCD order:
 // 72.0 us for the columns of 2^20-point transforms over 2^24 points on MI355X, against 90.8 us for
 // one tile per workgroup of 1024 lanes (8 values per lane, two waves per column) and 85.3 us for
@@ -161,6 +161,23 @@ template <int R, bool Inv, bool Table>
 void dispatch_strided_columns(int n, const StridedIo& io, long long batch, hipStream_t stream)
 {
     switch (n) {
+    case 64:
+    case 128:
+        // Wide matrices (the two-pass split's 64 x 512 and 128 x 512 at 2^15 and 2^16 points)
+        // run persistent with workgroups of 512 lanes, 64- or 32-column tiles (512- or 256-byte
+        // runs): over 2^24 points 56.8 -> 48.8 us at 64 and 63.8 -> 51.7 us at 128 on MI355X.
+        if (io.cols >= 256) {
+            if (n == 64) {
+                launch_columns_persistent<Plan<64, R, column_e<64, R>(), 512>, Inv, Table>(
+                    io, batch, stream);
+            } else {
+                launch_columns_persistent<Plan<128, R, column_e<128, R>(), 512>, Inv, Table>(
+                    io, batch, stream);
+            }
+        } else {
+            dispatch_columns<R, Inv, Table>(n, io, batch, stream);
+        }
+        break;
     case 256:
         // Wide matrices (the four-step's 256 x 16384 at 2^22 points) take workgroups of 1024
         // lanes, 32-column tiles with the radix-8 plans (256-byte runs): 59.7 -> 55.6 us; at 128

@@ -20,10 +20,10 @@ METHOD_IDS = [f"{impl}-{cols}" for impl, cols in METHODS]
 
 # (1024, 8) and (1024, 16): 1024-point strided columns, the persistent kernel in XCD order.
 SHAPES = [(1, 8), (8, 1), (2, 2), (16, 16), (64, 32), (8, 256), (256, 8), (4096, 4), (4, 4096),
-          (1024, 8)]
+          (1024, 8), (64, 512), (128, 256)]
 # (128, 128) and (512, 512) are BASELINE C3's grids, run here with both column methods.
 REAL_SHAPES = [(1, 8), (8, 2), (16, 16), (64, 32), (8, 256), (256, 8), (4096, 4), (2, 8192),
-               (128, 128), (512, 512), (1024, 16)]
+               (128, 128), (512, 512), (1024, 16), (64, 1024), (128, 512)]
 
 
 def cuda(x: np.ndarray) -> torch.Tensor:

@@ -60,6 +60,7 @@ CASES_2D = [
     (32, 128, 4, 20),
     (256, 256, 16, 16),
     (1024, 16, 100, 5),
+    (128, 1024, 16, 300),
     (4096, 2, 2, 2),
     (2, 8192, 1, 64),
     (128, 128, 16, 16),
