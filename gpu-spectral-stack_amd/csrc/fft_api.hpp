@@ -15,9 +15,10 @@ namespace spx {
 constexpr int kStockhamMaxN = 4096;                          // one kernel, LDS-resident
 constexpr int kFourStepMaxN = kStockhamMaxN * kStockhamMaxN;  // 2^24 (reference fft.hpp:18-21)
 // C2C sizes above kStockhamMaxN that still run as one kernel per transform (the whole transform
-// in one workgroup's LDS); the four-step split takes over beyond.
+// in one workgroup's LDS); the multi-pass splits take over beyond.
 constexpr int kSinglePassMaxN = 16384;
-// Above that, up to kTwoPassMaxN, a column pass and a row pass that stores transposed.
+// Above that, up to kTwoPassMaxN, a column pass and a row pass that stores transposed; beyond,
+// the column pass itself runs as two.
 constexpr int kTwoPassMaxN = 1 << 20;
 
 // reference fft.hpp:14-15, 36-39, 59-60
@@ -110,7 +111,7 @@ struct FftImpl {
 };
 
 // Scratch values c2c_work needs for batch transforms of n points: n x batch beyond the
-// single-pass sizes (the two-pass and four-step intermediates), none up to kSinglePassMaxN.
+// single-pass sizes (the two- and three-pass intermediates), none up to kSinglePassMaxN.
 std::size_t c2c_scratch_values(const FftImpl& impl, int n, int batch);
 
 // c2c that allocates nothing (noalloc.hip): large transforms use a static per-device scratch of

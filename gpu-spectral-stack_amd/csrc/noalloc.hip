@@ -1,6 +1,6 @@
 // c2c that allocates nothing, for callers that cannot allocate device memory (code being captured
 // into a HIP graph, tight serving loops, harnesses that forbid hipMalloc). It runs the same kernels
-// as c2c; the one difference is where the scratch of the large transforms (two-pass and four-step,
+// as c2c; the one difference is where the scratch of the large transforms (two and three passes,
 // n > kSinglePassMaxN: one intermediate of n x batch values) lives: in `scratch` below, a static
 // device array of kNoAllocScratchValues values (32 MiB) that every GPU the library runs on holds
 // from the library's load until the process ends.

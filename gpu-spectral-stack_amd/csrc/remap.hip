@@ -1,7 +1,7 @@
 // Index remaps: one pass that copies batch arrays through a row map and a column map, either in
-// the same orientation or transposed. It is the transpose of the 2D "transpose" method and of the
-// four-step, the gather of FNO modes out of a full half spectrum, and the scatter back (whose
-// zeros it writes in the same pass: every output value is written exactly once).
+// the same orientation or transposed. It is the transpose of the 2D "transpose" method, the
+// gather of FNO modes out of a full half spectrum, and the scatter back (whose zeros it writes in
+// the same pass: every output value is written exactly once).
 //
 // Design for gfx950 (wave64, LDS of 64 banks of 4 bytes, read by half-waves for 8-byte values):
 //
@@ -10,7 +10,7 @@
 //   its steps' loads in registers before touching LDS (every load in flight together), then
 //   writes them to the tile; after one barrier it reads tile columns and writes output rows,
 //   again 512 contiguous bytes per wave step. Against four waves of 16 steps: 2-5 % faster on
-//   the four-step's 1024 x 16384 and on 512 x 257 spectra, equal elsewhere; 16-byte accesses
+//   1024 x 16384 matrices and on 512 x 257 spectra, equal elsewhere; 16-byte accesses
 //   (pairs of values per lane) were 7-28 % slower.
 //   The tile is unpadded and XOR-swizzled: element (p, q) sits at p * 64 + (q ^ (p mod 32)).
 //   A half-wave writing a row (fixed p, 32 consecutive q) and a half-wave reading a column

@@ -179,8 +179,8 @@ void dispatch_strided_columns(int n, const StridedIo& io, long long batch, hipSt
         }
         break;
     case 256:
-        // Wide matrices (the four-step's 256 x 16384 at 2^22 points) take workgroups of 1024
-        // lanes, 32-column tiles with the radix-8 plans (256-byte runs): 59.7 -> 55.6 us; at 128
+        // Wide matrices take workgroups of 1024 lanes, 32-column tiles with the radix-8 plans
+        // (256-byte runs): 59.7 -> 55.6 us on 256 x 16384 matrices (2^22 points); at 128
         // columns (a 256^2 real array's) those measured 3 % slower than 16-column tiles.
         if (io.cols >= 1024) {
             launch_columns_persistent<Plan<256, R, column_e<256, R>(), 1024>, Inv, Table>(
@@ -629,7 +629,7 @@ struct Stockham {
     }
 
     // Any power of two up to kFourStepMaxN: one kernel up to kSinglePassMaxN, two passes up to
-    // kTwoPassMaxN, four steps beyond.
+    // kTwoPassMaxN, three beyond.
     // work: nullptr, or the caller's scratch of c2c_scratch_values(n, batch) values.
     static void c2c(const cf32* x, cf32* y, int n, int batch, Direction direction,
                     hipStream_t stream, cf32* work = nullptr)
@@ -663,38 +663,67 @@ struct Stockham {
             two_pass(x, y, n, batch, direction, stream, work);
             return;
         }
-        // Rows of kSinglePassMaxN points (one kernel each), so the columns are short (n1 <= 1024
-        // for n <= 2^24) and a column workgroup still reads runs of at least 64 bytes.
-        constexpr int n2 = kSinglePassMaxN;
+        three_pass(x, y, n, batch, direction, stream, work);
+    }
+
+    // n = n1 x 1024 for kTwoPassMaxN < n <= kFourStepMaxN (n1 = 2048 .. 16384): two_pass with
+    // its n1-point columns split again as 64 x n1b (ColumnStepIo, n1b = n1 / 64 = 32 .. 256).
+    // Pass A: 64-point transforms over rows j1 n1b + j2 of each n1 x 1024 matrix, twiddled by
+    // w_n1^(j2 k1) (x -> y); pass B: n1b-point transforms over rows k1 n1b + j2, written to row
+    // k1 + 64 k2 (y -> work); then two_pass's twiddled 1024-point rows, stored transposed
+    // (work -> y). Each pass stages whole column runs or transposes through LDS, so there is no
+    // separate transpose.
+    static void three_pass(const cf32* x, cf32* y, int n, int batch, Direction direction,
+                           hipStream_t stream, cf32* given)
+    {
+        constexpr int n2 = 1024;
+        constexpr int n1a = 64;
         const int n1 = n / n2;
-        if (static_cast<long long>(batch) * n1 > INT_MAX
-            || static_cast<long long>(batch) * n2 > INT_MAX) {
+        const int n1b = n1 / n1a;
+        if (static_cast<long long>(batch) * n1 > INT_MAX) {
             throw InvalidArgument("fourstep: too many transforms");
         }
         const bool inverse = direction == Direction::Inverse;
-        const CallScratch scratch(work, total, stream);
-        // 1. n1-point transforms down the n2 columns of each n1 x n2 matrix (x -> y).
-        columns_impl(x, y, n1, n2, batch, direction, stream, 0, 0, false);
-        // 2 + 3. Twiddle, then n2-point rows (y -> scratch).
-        const dev::TwiddleRowsIo rows{y,
-                                      scratch.get(),
-                                      inverse ? 1.0f / static_cast<float>(n2) : 1.0f,
-                                      inverse ? 1.0f : -1.0f,
-                                      n1,
-                                      2.0f / static_cast<float>(n)};
+        const float sign = inverse ? 1.0f : -1.0f;
+        const std::size_t total = static_cast<std::size_t>(n) * static_cast<std::size_t>(batch);
+        const CallScratch work(given, total, stream);
+        const long long wide = static_cast<long long>(n1b) * n2;
+        const dev::ColumnStepIo a{x,    y,    n2,   n1b,  n,    n2,    wide, n2,
+                                  wide, 1.0f, true, sign, 2.0f / static_cast<float>(n1),
+                                  true, false};
+        const dev::ColumnStepIo b{y,
+                                  work.get(),
+                                  n2,
+                                  n1a,
+                                  n,
+                                  wide,
+                                  n2,
+                                  n2,
+                                  static_cast<long long>(n1a) * n2,
+                                  inverse ? 1.0f / static_cast<float>(n1) : 1.0f,
+                                  false,
+                                  1.0f,
+                                  0.0f,
+                                  false,
+                                  false};
+        const long long transforms_a = static_cast<long long>(batch) * n1b * n2;
+        const long long transforms_b = static_cast<long long>(batch) * n1a * n2;
         if (inverse) {
-            dev::dispatch_large<R, true, Table>(n2, rows, static_cast<long long>(batch) * n1,
-                                                stream);
+            dev::dispatch_columns<R, true, Table>(n1a, a, transforms_a, stream);
+            dev::dispatch_columns<R, true, Table>(n1b, b, transforms_b, stream);
         } else {
-            dev::dispatch_large<R, false, Table>(n2, rows, static_cast<long long>(batch) * n1,
-                                                 stream);
+            dev::dispatch_columns<R, false, Table>(n1a, a, transforms_a, stream);
+            dev::dispatch_columns<R, false, Table>(n1b, b, transforms_b, stream);
         }
-        // 4. Row k1, column k2 holds X[k1 + n1 k2]: transpose each matrix (scratch -> y).
-        transpose(scratch.get(), y, n1, n2, batch, stream);
+        const dev::TwiddleRowsTransposedIo rows{
+            dev::TwiddleRowsIo{work.get(), y, inverse ? 1.0f / static_cast<float>(n2) : 1.0f,
+                               sign, n1, 2.0f / static_cast<float>(n)},
+            n};
+        launch_rows<n2>(rows, inverse, static_cast<long long>(batch) * n1, stream);
     }
 
-    // Columns of n = 2048 or 4096 points as two passes of 64 x (n / 64) (four-step on the column
-    // axis): a single pass would stage only 4 or 2 columns per workgroup, reading runs of 32 or
+    // Columns of n = 2048 or 4096 points as two passes of 64 x (n / 64) (a four-step split of
+    // the column axis): a single pass would stage only 4 or 2 columns per workgroup, reading runs of 32 or
     // 16 bytes; each of these passes stages 32 columns of 64 points (256-byte runs). Pass A runs
     // the 64-point transforms over rows j1 (n/64) + j2 and twiddles them (x -> work); pass B runs
     // the (n/64)-point transforms over rows k1 (n/64) + j2 and writes row k1 + 64 k2 (work -> y).

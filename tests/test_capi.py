@@ -436,7 +436,7 @@ def test_mode_gather_and_scatter_edges(lib, rng, n1, w, m1, m2):
                                                      (4, 3, 4096), (31, 40, 5), (1000, 20, 2),
                                                      (32, 32, 3)])
 def test_transpose_is_exact(lib, rng, rows, cols, batch):
-    # Partial tiles on both axes, a single column or row, and the four-step's 1024 x 16384; arrays
+    # Partial tiles on both axes, a single column or row, and a 1024 x 16384 matrix; arrays
     # with fewer than 32 rows or columns take the flat path (4 x 3: a 4 x 4 real transform's).
     x = (rng.standard_normal((batch, rows, cols)) + 1j * rng.standard_normal((batch, rows, cols)))
     xd = torch.from_numpy(x.astype(np.complex64)).cuda()

@@ -1,5 +1,5 @@
 """Complex 1D transforms against the float64 oracle, every implementation in spectral.FFT_IMPLS
-(reference tests/test_fft.py): every size 1 .. 4096 and batch, the four-step sizes up to 2^24,
+(reference tests/test_fft.py): every size 1 .. 4096 and batch, the multi-pass sizes up to 2^24,
 known answers, layouts, side streams and rejections."""
 
 import numpy as np
@@ -23,8 +23,9 @@ SIZES = [1, *POW2_SIZES]
 STOCKHAM = [impl for impl in IMPLS if impl.startswith("stockham")]
 # 8192 and 16384 run as one kernel per transform (a workgroup's LDS holds it); up to 2^20 as a
 # column pass and a transposing row pass (512-point rows up to 2^18, 1024-point beyond); larger
-# sizes as four steps with 16384-point rows.
-LARGE_SIZES = [8192, 16384, 32768, 1 << 16, 1 << 17, 1 << 18, 1 << 19, 1 << 20, 1 << 22]
+# sizes split the column pass in two (64 x n1/64 points) before the 1024-point rows.
+LARGE_SIZES = [8192, 16384, 32768, 1 << 16, 1 << 17, 1 << 18, 1 << 19, 1 << 20, 1 << 21, 1 << 22,
+               1 << 23]
 
 
 def run(x: np.ndarray, *, inverse: bool = False, impl: str) -> np.ndarray:
@@ -91,7 +92,7 @@ def test_single_pass_large_sizes_over_many_workgroups(rng, impl, n, batch, inver
 
 @pytest.mark.parametrize("impl", IMPLS)
 def test_largest_size(rng, impl):
-    n = 1 << 24  # 1024 x 16384 in the four-step split
+    n = 1 << 24  # 16384 x 1024: 64 x 256 column passes, then the rows
     x = random_complex(rng, (1, n))
     assert_transform_close(run(x, impl=impl), ref.fft(x), n)
 
@@ -109,7 +110,7 @@ def test_large_single_frequency_lands_in_one_bin(impl, n):
 
 @pytest.mark.parametrize("impl", STOCKHAM)
 def test_large_transform_on_a_side_stream(rng, impl):
-    # The four-step workspace is allocated and freed in stream order on the caller's stream.
+    # The two-pass workspace is allocated and freed in stream order on the caller's stream.
     x = torch.from_numpy(random_complex(rng, (2, 1 << 16))).cuda()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())

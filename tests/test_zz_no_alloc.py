@@ -44,7 +44,7 @@ def _both(lib, x: torch.Tensor, n: int, batch: int, inverse: int):
 
 
 def test_noalloc_matches_c2c_on_calls_in_a_row(lib, rng):
-    # The four-step path filling the whole static array, then the two-pass path filling it again,
+    # The three-pass path filling the whole static array, then the two-pass path filling it again,
     # then a smaller two-pass call and a single-pass size that needs no scratch: each must equal
     # spx_c2c bit for bit, whatever the array held from the call before.
     for n, batch in [(1 << 22, 1), (1 << 20, 4), (1 << 17, 3), (1024, 64)]:
