@@ -666,17 +666,20 @@ struct Stockham {
         three_pass(x, y, n, batch, direction, stream, work);
     }
 
-    // n = n1 x 1024 for kTwoPassMaxN < n <= kFourStepMaxN (n1 = 2048 .. 16384): two_pass with
-    // its n1-point columns split again as 64 x n1b (ColumnStepIo, n1b = n1 / 64 = 32 .. 256).
-    // Pass A: 64-point transforms over rows j1 n1b + j2 of each n1 x 1024 matrix, twiddled by
+    // n = n1 x 512 for kTwoPassMaxN < n <= kFourStepMaxN (n1 = 4096 .. 32768): two_pass with
+    // its n1-point columns split again as 64 x n1b (ColumnStepIo, n1b = n1 / 64 = 64 .. 512).
+    // Pass A: 64-point transforms over rows j1 n1b + j2 of each n1 x 512 matrix, twiddled by
     // w_n1^(j2 k1) (x -> y); pass B: n1b-point transforms over rows k1 n1b + j2, written to row
-    // k1 + 64 k2 (y -> work); then two_pass's twiddled 1024-point rows, stored transposed
-    // (work -> y). Each pass stages whole column runs or transposes through LDS, so there is no
-    // separate transpose.
+    // k1 + 64 k2 (y -> work); then two_pass's twiddled 512-point rows, 16 per workgroup, stored
+    // transposed in 128-byte runs (work -> y). Each pass stages whole column runs or transposes
+    // through LDS, so there is no separate transpose. Against the four-step it replaces (columns,
+    // 16384-point rows, transpose), over 2^24 points on MI355X: 2^22 158 -> 140 us, 2^24
+    // 183 -> 143 us; rows of 1024 (8 per workgroup, 64-byte runs) measured 3-7 % slower, and the
+    // persistent column kernel 4-12 % slower than one tile per workgroup for both steps.
     static void three_pass(const cf32* x, cf32* y, int n, int batch, Direction direction,
                            hipStream_t stream, cf32* given)
     {
-        constexpr int n2 = 1024;
+        constexpr int n2 = 512;
         constexpr int n1a = 64;
         const int n1 = n / n2;
         const int n1b = n1 / n1a;

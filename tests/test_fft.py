@@ -23,7 +23,7 @@ SIZES = [1, *POW2_SIZES]
 STOCKHAM = [impl for impl in IMPLS if impl.startswith("stockham")]
 # 8192 and 16384 run as one kernel per transform (a workgroup's LDS holds it); up to 2^20 as a
 # column pass and a transposing row pass (512-point rows up to 2^18, 1024-point beyond); larger
-# sizes split the column pass in two (64 x n1/64 points) before the 1024-point rows.
+# sizes split the column pass in two (64 x n1/64 points) before the 512-point rows.
 LARGE_SIZES = [8192, 16384, 32768, 1 << 16, 1 << 17, 1 << 18, 1 << 19, 1 << 20, 1 << 21, 1 << 22,
                1 << 23]
 
@@ -92,7 +92,7 @@ def test_single_pass_large_sizes_over_many_workgroups(rng, impl, n, batch, inver
 
 @pytest.mark.parametrize("impl", IMPLS)
 def test_largest_size(rng, impl):
-    n = 1 << 24  # 16384 x 1024: 64 x 256 column passes, then the rows
+    n = 1 << 24  # 32768 x 512: 64 x 512 column passes, then the rows
     x = random_complex(rng, (1, n))
     assert_transform_close(run(x, impl=impl), ref.fft(x), n)
 
