@@ -6,11 +6,17 @@
 //   fp32_gflops  independent FMA chains, no memory traffic (non-packed VALU FMA: packed FP32 is
 //                switched off in every build of this repository).
 //
+// --patterns times plain copies (no arithmetic) of the HBM access pattern of each pass of the hot
+// path, at that pass's size: contiguous rows in 16 KB workgroup chunks (the 1D kernels, the 2D
+// row-pair passes), and column tiles of T columns x N rows (the strided column passes). A pass
+// cannot stream faster than the copy of its own pattern, so each FFT pass is put against that.
+//
 // Same role as the reference's csrc/tools/peaks.cu:4-11 (achievable, not datasheet, peaks). The
 // copy kernel also serves as the calibration kernel of known size for the rocprof FETCH_SIZE /
 // WRITE_SIZE counters: `--copy-only --bytes B --iters K` runs exactly K copies of B bytes.
 //
 //   spectral_peaks [--copy-only] [--bytes B] [--iters K] [--out FILE]
+//   spectral_peaks --patterns
 
 #include <hip/hip_runtime.h>
 
@@ -61,6 +67,71 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ f2v load8(const f2v* p)
+{
+    if constexpr (NT) {
+        return __builtin_nontemporal_load(p);
+    } else {
+        return *p;
+    }
+}
+
+template <bool NT>
+__device__ __forceinline__ void store8(f2v* p, f2v v)
+{
+    if constexpr (NT) {
+        __builtin_nontemporal_store(v, p);
+    } else {
+        *p = v;
+    }
+}
+
+// Contiguous rows: workgroup b copies the Th * V 8-byte values from b Th V, lane t taking values
+// t + k Th (runs of 512 bytes per wave access). The grid covers the buffer exactly.
+template <int Th, int V, bool NT>
+__global__ void __launch_bounds__(Th) rows_copy_kernel(const f2v* __restrict__ in, f2v* __restrict__ out)
+{
+    const std::size_t base = static_cast<std::size_t>(blockIdx.x) * Th * V + threadIdx.x;
+    f2v v[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        v[k] = load8<NT>(in + base + static_cast<std::size_t>(k) * Th);
+    }
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        store8<NT>(out + base + static_cast<std::size_t>(k) * Th, v[k]);
+    }
+}
+
+// Column tiles: arrays of Rows x Cols 8-byte values; workgroup b copies the tile of T neighbouring
+// columns x Rows rows (tile b mod Cols / T of array b / (Cols / T)), lane t taking column t mod T
+// and rows t / T + k Th / T: runs of T * 8 bytes, one per row, Cols * 8 bytes apart.
+template <int Rows, int Cols, int T, int Th, bool NT>
+__global__ void __launch_bounds__(Th) tiles_copy_kernel(const f2v* __restrict__ in, f2v* __restrict__ out)
+{
+    constexpr int kTiles = Cols / T;
+    constexpr int kStep = Th / T;
+    constexpr int kK = Rows / kStep;
+    static_assert(Cols % T == 0 && Th % T == 0 && Rows % kStep == 0, "tile shape");
+    const std::size_t array = blockIdx.x / kTiles;
+    const int col = static_cast<int>(blockIdx.x % kTiles) * T + static_cast<int>(threadIdx.x) % T;
+    const int row = static_cast<int>(threadIdx.x) / T;
+    const std::size_t base = array * Rows * Cols + col + static_cast<std::size_t>(row) * Cols;
+    f2v v[kK];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) {
+        v[k] = load8<NT>(in + base + static_cast<std::size_t>(k) * kStep * Cols);
+    }
+#pragma unroll
+    for (int k = 0; k < kK; ++k) {
+        store8<NT>(out + base + static_cast<std::size_t>(k) * kStep * Cols, v[k]);
+    }
+}
+
 constexpr int kChains = 8;
 constexpr int kUnroll = 16;
 
@@ -98,6 +169,109 @@ float median(std::vector<float> v)
     return v[v.size() / 2];
 }
 
+// --patterns: each pattern copies `values` 8-byte values (in + out = 16 bytes per value) from
+// one buffer of a rotating set of four into another (1-2 GiB in all, beyond the 256 MB cache);
+// the patterns run interleaved over 7 rounds of 20 launches and each reports its median round.
+struct Pattern {
+    const char* name;
+    const char* serves;
+    std::size_t values;
+    void (*launch)(const f2v*, f2v*, hipStream_t);
+    std::vector<float> us;
+};
+
+template <int Th, int V, bool NT>
+void launch_rows(std::size_t values, const f2v* in, f2v* out, hipStream_t s)
+{
+    hipLaunchKernelGGL((rows_copy_kernel<Th, V, NT>), dim3(static_cast<unsigned>(values / (Th * V))),
+                       dim3(Th), 0, s, in, out);
+}
+
+template <int Rows, int Cols, int T, int Th, bool NT>
+void launch_tiles(std::size_t values, const f2v* in, f2v* out, hipStream_t s)
+{
+    hipLaunchKernelGGL((tiles_copy_kernel<Rows, Cols, T, Th, NT>),
+                       dim3(static_cast<unsigned>(values / (static_cast<std::size_t>(Rows) * T))),
+                       dim3(Th), 0, s, in, out);
+}
+
+constexpr std::size_t k2e24 = std::size_t(1) << 24;
+constexpr std::size_t k2e23 = std::size_t(1) << 23;
+
+int run_patterns()
+{
+    std::vector<Pattern> ps = {
+        {"rows 16 KB chunks, nontemporal", "C1 C2C n = 1024 (2^24 points)", k2e24,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, true>(k2e24, i, o, s); }, {}},
+        {"rows 16 KB chunks, plain", "2^24 points, plain accesses", k2e24,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, false>(k2e24, i, o, s); }, {}},
+        {"rows 16 KB chunks, nontemporal", "one pass of C3 512^2 x 64 (2^23 values)", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, true>(k2e23, i, o, s); }, {}},
+        {"rows 16 KB chunks, plain", "C3 512^2 row-pair pass (2^23 values)", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, false>(k2e23, i, o, s); }, {}},
+        {"tiles 16 x 512 of 512 x 256, plain", "C3 512^2 column pass (128-byte runs)", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<512, 256, 16, 1024, false>(k2e23, i, o, s); }, {}},
+        {"tiles 16 x 512 of 512 x 256, nontemporal", "C3 512^2 column pass, nontemporal", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<512, 256, 16, 1024, true>(k2e23, i, o, s); }, {}},
+        {"tiles 32 x 512 of 512 x 256, plain", "256-byte runs", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<512, 256, 32, 1024, false>(k2e23, i, o, s); }, {}},
+        {"tiles 64 x 512 of 512 x 256, plain", "512-byte runs", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<512, 256, 64, 1024, false>(k2e23, i, o, s); }, {}},
+        {"tiles 8 x 1024 of 1024 x 1024, plain", "2^20-point C2C column pass (64-byte runs)", k2e24,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<1024, 1024, 8, 512, false>(k2e24, i, o, s); }, {}},
+        {"tiles 16 x 1024 of 1024 x 1024, plain", "128-byte runs", k2e24,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<1024, 1024, 16, 1024, false>(k2e24, i, o, s); }, {}},
+    };
+    constexpr int kSets = 4;
+    const std::size_t bytes = k2e24 * sizeof(f2v);
+    f2v* in[kSets];
+    f2v* out[kSets];
+    for (int s = 0; s < kSets; ++s) {
+        CHECK(hipMalloc(&in[s], bytes));
+        CHECK(hipMalloc(&out[s], bytes));
+        CHECK(hipMemset(in[s], 0x3c, bytes));
+        CHECK(hipMemset(out[s], 0, bytes));
+    }
+    hipStream_t stream;
+    CHECK(hipStreamCreate(&stream));
+    hipEvent_t e0, e1;
+    CHECK(hipEventCreate(&e0));
+    CHECK(hipEventCreate(&e1));
+    constexpr int kIters = 20;
+    for (auto& p : ps) {
+        for (int i = 0; i < 3; ++i) {
+            p.launch(in[i % kSets], out[i % kSets], stream);
+        }
+    }
+    CHECK(hipGetLastError());
+    CHECK(hipStreamSynchronize(stream));
+    for (int r = 0; r < 7; ++r) {
+        for (auto& p : ps) {
+            CHECK(hipEventRecord(e0, stream));
+            for (int i = 0; i < kIters; ++i) {
+                p.launch(in[i % kSets], out[i % kSets], stream);
+            }
+            CHECK(hipEventRecord(e1, stream));
+            CHECK(hipEventSynchronize(e1));
+            float ms = 0.0f;
+            CHECK(hipEventElapsedTime(&ms, e0, e1));
+            p.us.push_back(1000.0f * ms / kIters);
+        }
+    }
+    CHECK(hipGetLastError());
+    std::printf("| pattern | size | serves | us | GB/s |\n|---|---:|---|---:|---:|\n");
+    for (auto& p : ps) {
+        const double us = median(p.us);
+        std::printf("| %s | %.0f MiB in + out | %s | %.2f | %.1f |\n", p.name,
+                    p.values * 16.0 / (1 << 20), p.serves, us, p.values * 16.0 / (us * 1e3));
+    }
+    for (int s = 0; s < kSets; ++s) {
+        CHECK(hipFree(in[s]));
+        CHECK(hipFree(out[s]));
+    }
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv)
@@ -108,7 +282,9 @@ int main(int argc, char** argv)
     const char* out_path = nullptr;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
-        if (a == "--copy-only") {
+        if (a == "--patterns") {
+            return run_patterns();
+        } else if (a == "--copy-only") {
             copy_only = true;
         } else if (a == "--bytes" && i + 1 < argc) {
             bytes = std::strtoull(argv[++i], nullptr, 10);
@@ -118,7 +294,7 @@ int main(int argc, char** argv)
             out_path = argv[++i];
         } else {
             std::fprintf(stderr, "usage: spectral_peaks [--copy-only] [--bytes B] [--iters K] "
-                                 "[--out FILE]\n");
+                                 "[--out FILE] | --patterns\n");
             return 2;
         }
     }
