@@ -283,27 +283,44 @@ struct FullRows {
     static_assert(!kUse || (RPW % RW == 0 && RPW <= 64 && kSteps * CW <= 16),
                   "whole rows per wave, the Nyquist bins in one step");
 
-    // src: the workgroup's first array; rows of arrays >= count read the last row instead.
+    // A wave's rows stay inside one 16-row block of the padded tile (rows RPW-aligned, RPW a
+    // divisor of 16, one row per step), or the tile is unpadded: either way step i's tile row is
+    // the lane's first plus i RW TS, a compile-time offset.
+    static constexpr bool kLinearRows = !F::kPadRows || (RW == 1 && 16 % RPW == 0);
+
+    // src: the workgroup's first array; rows of arrays >= count read the last row instead. With
+    // one array per workgroup count is 1 and every row exists, so the addresses are the lane's
+    // own plus compile-time offsets (no clamp).
     __device__ __forceinline__ static void load(cf32* tile, const cf32* src, int count, int tid)
     {
         const int row = (tid / 64) * RPW + (tid % 64) / (F::M >= 64 ? 64 : F::M);
         const int col = F::M >= 64 ? tid % 64 : tid % F::M;
         const int last = count * F::N1 - 1;
+        const cf32* const lane_src = src + row * kPitch + col;
         cf32 val[kSteps][CW];
         static_for<0, kSteps>([&](auto ii) {
             constexpr int i = decltype(ii)::value;
             static_for<0, CW>([&](auto jj) {
                 constexpr int j = decltype(jj)::value;
-                val[i][j] = src[cmin(row + i * RW, last) * kPitch + col + 64 * j];
+                if constexpr (F::AP == 1) {
+                    val[i][j] = lane_src[i * RW * kPitch + 64 * j];
+                } else {
+                    val[i][j] = src[cmin(row + i * RW, last) * kPitch + col + 64 * j];
+                }
             });
         });
         const int nrow = cmin((tid / 64) * RPW + tid % 64, F::kRows - 1);
         const cf32 ny = src[cmin(nrow, last) * kPitch + F::M];
+        cf32* const lane_tile = tile + F::row_at(row) + pad(col);
         static_for<0, kSteps>([&](auto ii) {
             constexpr int i = decltype(ii)::value;
             static_for<0, CW>([&](auto jj) {
                 constexpr int j = decltype(jj)::value;
-                tile[F::row_at(row + i * RW) + pad(col + 64 * j)] = val[i][j];
+                if constexpr (kLinearRows) {
+                    lane_tile[i * RW * F::TS + pad(64 * j)] = val[i][j];
+                } else {
+                    tile[F::row_at(row + i * RW) + pad(col + 64 * j)] = val[i][j];
+                }
             });
         });
         if (tid % 64 < RPW) {
@@ -351,14 +368,18 @@ __device__ __forceinline__ void store_full(const cf32* tile, cf32* dst, int coun
 
 // Forward: z = the real arrays viewed as complex (batch x N1 x M), y = batch arrays of rows_out x w
 // values (rows_out = 2 m1 when m1 > 0, else N1). wdiv divides by w, odiv by rows_out w.
-template <class F>
+template <class F, bool Full = false>
 __global__ void __launch_bounds__(F::NT)
-    rfft2_fused_kernel(const cf32* __restrict__ z, cf32* __restrict__ y, int m1, int w,
+    rfft2_fused_kernel(const cf32* __restrict__ z, cf32* __restrict__ y, int m1_arg, int w_arg,
                        FastDiv wdiv, FastDiv odiv, long long batch, const cf32* table)
 {
     using PR = typename F::PR;
     using PC = typename F::PC;
     __shared__ cf32 tile[F::AP * F::kTile];
+    // Full: the whole half spectrum (m1 = 0, w = M + 1) as compile-time facts, so the combine's
+    // bounds and the store's route fold away.
+    const int m1 = Full ? 0 : m1_arg;
+    const int w = Full ? F::M + 1 : w_arg;
 
     const long long first = static_cast<long long>(blockIdx.x) * F::AP;
     const int count = static_cast<int>(batch - first < F::AP ? batch - first : F::AP);
@@ -469,14 +490,18 @@ __global__ void __launch_bounds__(F::NT)
 // Inverse: x = batch arrays of rows_in x w values (rows_in = 2 m1 when m1 > 0, else N1; the other
 // frequencies are zero), z = the real outputs viewed as complex (batch x N1 x M). wdiv divides by
 // w, adiv by rows_in w.
-template <class F>
+template <class F, bool Full = false>
 __global__ void __launch_bounds__(F::NT)
-    irfft2_fused_kernel(const cf32* __restrict__ x, cf32* __restrict__ z, int m1, int w,
+    irfft2_fused_kernel(const cf32* __restrict__ x, cf32* __restrict__ z, int m1_arg, int w_arg,
                         FastDiv wdiv, FastDiv adiv, long long batch, const cf32* table)
 {
     using PR = typename F::PR;
     using PC = typename F::PC;
     __shared__ cf32 tile[F::AP * F::kTile];
+    // Full: the whole half spectrum (m1 = 0, w = M + 1) as compile-time facts, so the column
+    // reads and the prepare's bounds fold away.
+    const int m1 = Full ? 0 : m1_arg;
+    const int w = Full ? F::M + 1 : w_arg;
 
     const long long first = static_cast<long long>(blockIdx.x) * F::AP;
     const int count = static_cast<int>(batch - first < F::AP ? batch - first : F::AP);

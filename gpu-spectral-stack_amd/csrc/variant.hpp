@@ -1028,8 +1028,12 @@ struct Fused2dDriver {
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
         const cf32* table = Table ? twiddle_table() : nullptr;
         const int rows_out = m1 > 0 ? 2 * m1 : N1;
-        hipLaunchKernelGGL((dev::rfft2_fused_kernel<F>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(F::NT), 0, stream, reinterpret_cast<const cf32*>(x), y, m1, w,
+        // The whole half spectrum (rfft2 itself) takes the variant with m1 and w fixed at
+        // compile time.
+        const auto kernel = (m1 == 0 && w == M + 1) ? dev::rfft2_fused_kernel<F, true>
+                                                    : dev::rfft2_fused_kernel<F, false>;
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(F::NT), 0, stream,
+                           reinterpret_cast<const cf32*>(x), y, m1, w,
                            dev::FastDiv::of(static_cast<unsigned>(w)),
                            dev::FastDiv::of(static_cast<unsigned>(rows_out * w)),
                            static_cast<long long>(batch), table);
@@ -1055,8 +1059,10 @@ struct Fused2dDriver {
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
         const cf32* table = Table ? twiddle_table() : nullptr;
         const int rows_in = m1 > 0 ? 2 * m1 : N1;
-        hipLaunchKernelGGL((dev::irfft2_fused_kernel<F>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(F::NT), 0, stream, x, reinterpret_cast<cf32*>(y), m1, w,
+        const auto kernel = (m1 == 0 && w == M + 1) ? dev::irfft2_fused_kernel<F, true>
+                                                    : dev::irfft2_fused_kernel<F, false>;
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(F::NT), 0, stream, x,
+                           reinterpret_cast<cf32*>(y), m1, w,
                            dev::FastDiv::of(static_cast<unsigned>(w)),
                            dev::FastDiv::of(static_cast<unsigned>(rows_in * w)),
                            static_cast<long long>(batch), table);
