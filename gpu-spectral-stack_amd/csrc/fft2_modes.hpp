@@ -147,11 +147,15 @@ __global__ void __launch_bounds__(F::NT)
 
 // Inverse: x = batch arrays of 2 m1 x w modes (the other frequencies zero), z = the real outputs
 // viewed as complex (batch x N1 x M). wdiv divides by w.
-template <class F>
+// W: a compile-time bound on w (w <= W <= WMax, W a power of two), so that which of a lane's row
+// slots can hold a kept bin is known at compile time; tile columns w .. W-1 are zeroed first.
+template <class F, int W>
 __global__ void __launch_bounds__(F::NT)
     irfft2_modes_kernel(const cf32* __restrict__ x, cf32* __restrict__ z, int m1, int w,
                         FastDiv wdiv, const cf32* table)
 {
+    static_assert(W >= 1 && W <= F::WMax && (W & (W - 1)) == 0 && F::NT % W == 0,
+                  "W is a power of two within the tile's columns");
     using PR = typename F::PR;
     using PC = typename F::PC;
     __shared__ cf32 lds[F::kScratch + F::kTile];
@@ -175,6 +179,16 @@ __global__ void __launch_bounds__(F::NT)
             const int e = cmin(tid + k * F::NT, total - 1);
             const int f = static_cast<int>(wdiv.div(static_cast<unsigned>(e)));
             tile[F::tile_row(F::row_of(f, m1)) + (e - f * w)] = val[k];
+        }
+    }
+    // Columns w .. W-1 of every row are zeros, read as such by the row prepare below (the column
+    // pass touches only columns below w).
+    if (w < W) {
+        const int c = tid % W;
+        if (c >= w) {
+            for (int f = tid / W; f < F::N1; f += F::NT / W) {
+                tile[F::tile_row(f) + c] = czero();
+            }
         }
     }
     __syncthreads();
@@ -210,8 +224,8 @@ __global__ void __launch_bounds__(F::NT)
     // O = exp(pi i k / M) (X[k] - conj X[M-k]) / 2, from the tile row (X[k] = 0 for k >= w; the
     // imaginary part of X[0] dropped; X[M] is never kept, w < M). The scale 1 / (N1 M), which
     // with the halves makes the row inverse numpy's irfft and covers both passes, rides on the
-    // halves. A slot whose k lies in [w, M - w] for every lane of the row is zero (a test
-    // uniform over the workgroup).
+    // halves. A slot whose k lies in [W, M - W] for every lane of the row is zero, known at
+    // compile time; the tile's columns w .. W-1 hold zeros, so reads below W need no test of w.
     constexpr float half = 0.5f / static_cast<float>(F::N1 * F::M);
     constexpr int R0 = PR::template radix<0>();
     const int lane = tid % PR::L;
@@ -227,13 +241,13 @@ __global__ void __launch_bounds__(F::NT)
         static_for<0, PR::E>([&](auto ei) {
             constexpr int e = decltype(ei)::value;
             constexpr int off = (e / R0) * PR::L + (e % R0) * (PR::N / R0);
-            if (off >= w && F::M - off - (PR::L - 1) >= w) {
+            if constexpr (off >= W && F::M - off - (PR::L - 1) >= W) {
                 v[e] = czero();
                 return;
             }
             const int k = lane + off;
-            cf32 xk = k < w ? trow[k] : czero();
-            const cf32 xm = (k > 0 && F::M - k < w) ? trow[F::M - k] : czero();
+            cf32 xk = k < W ? trow[k] : czero();
+            const cf32 xm = (k > 0 && F::M - k < W) ? trow[F::M - k] : czero();
             if (k == 0) {
                 xk.im = 0.0f;
             }

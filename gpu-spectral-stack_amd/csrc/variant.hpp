@@ -1046,9 +1046,11 @@ struct Fused2dDriver {
         if constexpr (modes_shape<N1, 2 * M>()) {
             if (m1 > 0 && w <= M / 4) {
                 using F = dev::Modes2d<N1, M, R, Table>;
-                hipLaunchKernelGGL((dev::irfft2_modes_kernel<F>),
-                                   dim3(static_cast<unsigned>(batch)), dim3(F::NT), 0, stream, x,
-                                   reinterpret_cast<cf32*>(y), m1, w,
+                // A compile-time bound on w: half the tile's columns, or all of them.
+                const auto kernel = w <= F::WMax / 2 ? dev::irfft2_modes_kernel<F, F::WMax / 2>
+                                                     : dev::irfft2_modes_kernel<F, F::WMax>;
+                hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(batch)), dim3(F::NT), 0,
+                                   stream, x, reinterpret_cast<cf32*>(y), m1, w,
                                    dev::FastDiv::of(static_cast<unsigned>(w)),
                                    Table ? twiddle_table() : nullptr);
                 SPX_LAUNCH_CHECK();
