@@ -147,15 +147,19 @@ __global__ void __launch_bounds__(F::NT)
 
 // Inverse: x = batch arrays of 2 m1 x w modes (the other frequencies zero), z = the real outputs
 // viewed as complex (batch x N1 x M). wdiv divides by w.
-// W: a compile-time bound on w (w <= W <= WMax, W a power of two), so that which of a lane's row
-// slots can hold a kept bin is known at compile time; tile columns w .. W-1 are zeroed first.
-template <class F, int W>
+// W and M1: compile-time bounds on w and m1 (w <= W <= WMax, m1 <= M1 <= N1 / 2, powers of two),
+// so that which of a lane's row slots and column slots can hold a kept mode is known at compile
+// time and the others are constant zeros in the first stages. Tile columns w .. W-1, and tile
+// rows m1 .. M1-1 and N1-M1 .. N1-m1-1 of the kept columns, are zeroed with the load.
+template <class F, int W, int M1>
 __global__ void __launch_bounds__(F::NT)
     irfft2_modes_kernel(const cf32* __restrict__ x, cf32* __restrict__ z, int m1, int w,
                         FastDiv wdiv, const cf32* table)
 {
     static_assert(W >= 1 && W <= F::WMax && (W & (W - 1)) == 0 && F::NT % W == 0,
                   "W is a power of two within the tile's columns");
+    static_assert(M1 >= 1 && 2 * M1 <= F::N1 && (M1 & (M1 - 1)) == 0,
+                  "M1 is a power of two, at most half the rows");
     using PR = typename F::PR;
     using PC = typename F::PC;
     __shared__ cf32 lds[F::kScratch + F::kTile];
@@ -191,10 +195,19 @@ __global__ void __launch_bounds__(F::NT)
             }
         }
     }
+    if (m1 < M1) {
+        // Row q of the 2 (M1 - m1) rows to clear: m1 + q, then N1 - M1 + (q - (M1 - m1)).
+        const int gap = M1 - m1;
+        for (int e = tid; e < 2 * gap * w; e += F::NT) {
+            const int q = static_cast<int>(wdiv.div(static_cast<unsigned>(e)));
+            const int f = q < gap ? m1 + q : F::N1 - M1 + (q - gap);
+            tile[F::tile_row(f) + (e - q * w)] = czero();
+        }
+    }
     __syncthreads();
 
-    // Inverse columns 0 .. w-1 in place; rows not kept are read as zeros (every row of a column
-    // is overwritten by its transform).
+    // Inverse columns 0 .. w-1 in place; rows past the bound M1 are read as zeros (every row of a
+    // column is overwritten by its transform).
     constexpr int CPP = F::NT / PC::L;
     constexpr int RC = PC::template radix<0>();
 #pragma unroll 1
@@ -210,7 +223,7 @@ __global__ void __launch_bounds__(F::NT)
                 for (int r = 0; r < RC; ++r) {
                     const int i = input_index<PC, 0>(clane, b, r);
                     u[b * RC + r] =
-                        (i < m1 || i >= F::N1 - m1) ? col[F::ColLay::at(i)] : czero();
+                        (i < M1 || i >= F::N1 - M1) ? col[F::ColLay::at(i)] : czero();
                 }
             }
             run_stages<PC, 0, true, F::kTable, typename F::ColLay>(u, col, clane, table);

@@ -1046,9 +1046,17 @@ struct Fused2dDriver {
         if constexpr (modes_shape<N1, 2 * M>()) {
             if (m1 > 0 && w <= M / 4) {
                 using F = dev::Modes2d<N1, M, R, Table>;
-                // A compile-time bound on w: half the tile's columns, or all of them.
-                const auto kernel = w <= F::WMax / 2 ? dev::irfft2_modes_kernel<F, F::WMax / 2>
-                                                     : dev::irfft2_modes_kernel<F, F::WMax>;
+                // Compile-time bounds on w (half the tile's columns, or all of them) and on m1
+                // (an eighth, a quarter or half of the rows): the smallest that hold them.
+                const auto pick = [m1](auto wb) {
+                    constexpr int kW = decltype(wb)::value;
+                    return m1 <= N1 / 8   ? dev::irfft2_modes_kernel<F, kW, N1 / 8>
+                           : m1 <= N1 / 4 ? dev::irfft2_modes_kernel<F, kW, N1 / 4>
+                                          : dev::irfft2_modes_kernel<F, kW, N1 / 2>;
+                };
+                const auto kernel = w <= F::WMax / 2
+                                        ? pick(std::integral_constant<int, F::WMax / 2>{})
+                                        : pick(std::integral_constant<int, F::WMax>{});
                 hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(batch)), dim3(F::NT), 0,
                                    stream, x, reinterpret_cast<cf32*>(y), m1, w,
                                    dev::FastDiv::of(static_cast<unsigned>(w)),

@@ -86,6 +86,31 @@ def test_irfft2_from_modes_matches_the_oracle(rng, impl, n1, n2, m1, m2):
     assert_transform_close(y, ref.irfft2_from_modes(modes, (n1, n2)), n1 * n2, axes=AXES)
 
 
+# Every shape with a narrow-tile single-pass pruned kernel (at most n2/8 kept columns). Their
+# inverse is built for compile-time bounds on the kept columns (n2/16 or n2/8) and rows (n1/8,
+# n1/4 or n1/2): each case sits at a bound or just past one, in both directions.
+NARROW_SHAPES = [(64, 64), (128, 64), (32, 128), (64, 128), (128, 128), (32, 256), (64, 256)]
+
+
+def narrow_cases():
+    for n1, n2 in NARROW_SHAPES:
+        wmax = n2 // 8
+        for m2 in sorted({1, wmax // 2, wmax // 2 + 1, wmax}):
+            for m1 in sorted({1, n1 // 8, n1 // 8 + 1, n1 // 4 + 1, n1 // 2}):
+                yield n1, n2, m1, m2
+
+
+@pytest.mark.parametrize("impl", ["stockham_r4", "stockham_r8", "stockham_r8_table"])
+@pytest.mark.parametrize(("n1", "n2", "m1", "m2"), list(narrow_cases()))
+def test_narrow_tile_kernels_at_their_bounds(rng, impl, n1, n2, m1, m2):
+    x = random_real(rng, (3, n1, n2))
+    y = spectral.rfft2_truncated(cuda(x), m1, m2, impl=impl)
+    assert_transform_close(y, ref.rfft2_truncate(x, m1, m2), n1 * n2, axes=AXES)
+    modes = random_complex(rng, (3, 2 * m1, m2))
+    back = spectral.irfft2_from_modes(cuda(modes), (n1, n2), impl=impl)
+    assert_transform_close(back, ref.irfft2_from_modes(modes, (n1, n2)), n1 * n2, axes=AXES)
+
+
 def golden_positions(n1: int, n2: int, m1: int, m2: int) -> np.ndarray:
     data = json.loads((Path(__file__).parent / "golden" / "modes_index.json").read_text())
     case = next(c for c in data if (c["n1"], c["n2"], c["m1"], c["m2"]) == (n1, n2, m1, m2))
