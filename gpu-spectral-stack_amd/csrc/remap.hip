@@ -20,6 +20,10 @@
 // * Not transposed: each output row is walked by a power-of-two group of lanes as wide as the row
 //   (up to a wave), so short rows (16 modes) still fill whole waves with several rows each. The
 //   row and column maps are evaluated per lane; no flat-index division per value.
+// * Transposed, a size of 64k + 1 (a real spectrum's n/2 + 1 values): the last full tile's
+//   workgroup also copies the one row or column past it, straight from HBM to HBM, so no
+//   workgroup carries a 64 x 1 sliver tile (whose 64 strided loads and near-idle lanes made
+//   128 x 65 transposes take 37.7 us against 26.0 us for 128 x 64; now 28.3 us).
 // * Transposed, arrays with fewer than 32 rows or columns: one lane per output value, the arrays
 //   walked flat (stores coalesced; an array's reads stay within a few cache lines). A 64 x 64 tile
 //   per array would leave most of each workgroup idle: at 4 x 3 arrays (2^24-point 4 x 4 real
@@ -41,9 +45,13 @@ constexpr long long kMaxBlocks = 1 << 20;        // the loops below cover any re
 
 __device__ __forceinline__ cf32 zero() { return cf32{0.0f, 0.0f}; }
 
+// extra_p / extra_q: the output has one column / row past its last full tile (a width of
+// 64k + 1, as a real spectrum's n/2 + 1 values): the workgroup of that last tile copies it
+// directly, one value per lane, instead of a workgroup per sliver tile of 64 x 1 (which made
+// 128 x 65 transposes 45 % slower than 128 x 64 ones).
 __global__ void __launch_bounds__(kTileThreads)
     remap_tiles_kernel(const cf32* __restrict__ x, cf32* __restrict__ y, Remap r, int tiles_p,
-                       int tiles_q, long long tiles)
+                       int tiles_q, long long tiles, int extra_p, int extra_q)
 {
     __shared__ cf32 tile[kTile * kTile];
     const int lane = static_cast<int>(threadIdx.x) & 63;
@@ -53,7 +61,8 @@ __global__ void __launch_bounds__(kTileThreads)
         const long long b = t / per_array;
         const int rest = static_cast<int>(t - b * per_array);
         const int tq = rest / tiles_p;
-        const int p0 = (rest - tq * tiles_p) * kTile;  // output columns = input rows
+        const int tp = rest - tq * tiles_p;
+        const int p0 = tp * kTile;  // output columns = input rows
         const int q0 = tq * kTile;                      // output rows = input columns
         const cf32* xs = x + b * r.x_array;
 
@@ -87,6 +96,31 @@ __global__ void __launch_bounds__(kTileThreads)
             if (q < r.y_rows && p_out < r.y_cols) {
                 ys[static_cast<long long>(q) * r.y_cols + p_out] = v[k];
             }
+        }
+        // The extra output row (input column y_rows - 1) across this tile's columns: wave 0. The
+        // extra output column (input row y_cols - 1) across its rows: wave 1. Their corner: wave 2.
+        const bool last_q = extra_q != 0 && tq == tiles_q - 1;
+        const bool last_p = extra_p != 0 && tp == tiles_p - 1;
+        if (last_q && wave == 0 && p_out < r.y_cols - extra_p) {
+            const int q = r.y_rows - 1;
+            const int xr = r.rows(p_out);
+            const int xc2 = r.cols(q);
+            ys[static_cast<long long>(q) * r.y_cols + p_out] =
+                (xr >= 0 && xc2 >= 0) ? xs[static_cast<long long>(xr) * r.x_pitch + xc2] : zero();
+        }
+        if (last_p && wave == 1 && q0 + lane < r.y_rows - extra_q) {
+            const int p = r.y_cols - 1;
+            const int q = q0 + lane;
+            const int xr = r.rows(p);
+            const int xc2 = r.cols(q);
+            ys[static_cast<long long>(q) * r.y_cols + p] =
+                (xr >= 0 && xc2 >= 0) ? xs[static_cast<long long>(xr) * r.x_pitch + xc2] : zero();
+        }
+        if (last_p && last_q && wave == 2 && lane == 0) {
+            const int xr = r.rows(r.y_cols - 1);
+            const int xc2 = r.cols(r.y_rows - 1);
+            ys[static_cast<long long>(r.y_rows - 1) * r.y_cols + r.y_cols - 1] =
+                (xr >= 0 && xc2 >= 0) ? xs[static_cast<long long>(xr) * r.x_pitch + xc2] : zero();
         }
         __syncthreads();  // the next tile overwrites the LDS
     }
@@ -160,11 +194,14 @@ void remap(const cf32* x, cf32* y, const Remap& r, bool transposed, hipStream_t 
                                static_cast<unsigned long long>(total));
         }
     } else if (transposed) {
-        const int tiles_p = (r.y_cols + kTile - 1) / kTile;
-        const int tiles_q = (r.y_rows + kTile - 1) / kTile;
+        // Sizes here are at least 32, so a size of 64k + 1 has k >= 1 full tiles.
+        const int extra_p = r.y_cols % kTile == 1 ? 1 : 0;
+        const int extra_q = r.y_rows % kTile == 1 ? 1 : 0;
+        const int tiles_p = (r.y_cols - extra_p + kTile - 1) / kTile;
+        const int tiles_q = (r.y_rows - extra_q + kTile - 1) / kTile;
         const long long tiles = static_cast<long long>(tiles_p) * tiles_q * r.batch;
         hipLaunchKernelGGL(remap_tiles_kernel, dim3(blocks(tiles)), dim3(kTileThreads), 0, stream,
-                           x, y, r, tiles_p, tiles_q, tiles);
+                           x, y, r, tiles_p, tiles_q, tiles, extra_p, extra_q);
     } else {
         int lanes_log2 = 0;
         while (lanes_log2 < 6 && (1 << lanes_log2) < r.y_cols) {

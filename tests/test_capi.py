@@ -434,10 +434,14 @@ def test_mode_gather_and_scatter_edges(lib, rng, n1, w, m1, m2):
 @pytest.mark.parametrize(("rows", "cols", "batch"), [(1, 1, 3), (64, 64, 2), (65, 63, 3),
                                                      (1024, 16384, 1), (3, 200, 7), (513, 1, 2),
                                                      (4, 3, 4096), (31, 40, 5), (1000, 20, 2),
-                                                     (32, 32, 3)])
+                                                     (32, 32, 3), (128, 65, 5), (65, 128, 5),
+                                                     (257, 512, 2), (512, 257, 2), (65, 65, 3),
+                                                     (129, 193, 2), (33, 65, 3), (65, 40, 3)])
 def test_transpose_is_exact(lib, rng, rows, cols, batch):
     # Partial tiles on both axes, a single column or row, and a 1024 x 16384 matrix; arrays
     # with fewer than 32 rows or columns take the flat path (4 x 3: a 4 x 4 real transform's).
+    # Sizes of 64k + 1 (a real spectrum's n/2 + 1) have their last row or column copied by the
+    # last full tile's workgroup, alone, with the other axis full or partial, and both at once.
     x = (rng.standard_normal((batch, rows, cols)) + 1j * rng.standard_normal((batch, rows, cols)))
     xd = torch.from_numpy(x.astype(np.complex64)).cuda()
     yd = torch.empty(batch, cols, rows, dtype=torch.complex64, device="cuda")
