@@ -24,6 +24,9 @@
 //   workgroup also copies the one row or column past it, straight from HBM to HBM, so no
 //   workgroup carries a 64 x 1 sliver tile (whose 64 strided loads and near-idle lanes made
 //   128 x 65 transposes take 37.7 us against 26.0 us for 128 x 64; now 28.3 us).
+// * Output rows that do not start on 128-byte lines (a width not a multiple of 16 values): runs of
+//   8 consecutive tiles go to one XCD (xcd_grouped), so the partial lines that neighbouring tiles
+//   share meet in one L2: 257 x 512 -> 512 x 257 went 33.0 -> 28.4 us.
 // * Transposed, arrays with fewer than 32 rows or columns: one lane per output value, the arrays
 //   walked flat (stores coalesced; an array's reads stay within a few cache lines). A 64 x 64 tile
 //   per array would leave most of each workgroup idle: at 4 x 3 arrays (2^24-point 4 x 4 real
@@ -49,15 +52,31 @@ __device__ __forceinline__ cf32 zero() { return cf32{0.0f, 0.0f}; }
 // 64k + 1, as a real spectrum's n/2 + 1 values): the workgroup of that last tile copies it
 // directly, one value per lane, instead of a workgroup per sliver tile of 64 x 1 (which made
 // 128 x 65 transposes 45 % slower than 128 x 64 ones).
+// Workgroup b runs on XCD b mod 8, each XCD with its own L2. With group > 1, each span of
+// 8 group workgroups is renumbered so that every XCD takes `group` consecutive tiles (tiles
+// next to each other in the output, which share the partial cache lines of rows that do not
+// start on a line); a trailing partial span keeps its order.
+__device__ __forceinline__ long long xcd_grouped(long long b, long long grid, int group)
+{
+    const long long span = 8LL * group;
+    if (group <= 1 || b >= grid / span * span) {
+        return b;
+    }
+    const long long base = b / span * span;
+    const long long rest = b - base;
+    return base + (rest % 8) * group + rest / 8;
+}
+
 __global__ void __launch_bounds__(kTileThreads)
     remap_tiles_kernel(const cf32* __restrict__ x, cf32* __restrict__ y, Remap r, int tiles_p,
-                       int tiles_q, long long tiles, int extra_p, int extra_q)
+                       int tiles_q, long long tiles, int extra_p, int extra_q, int group)
 {
     __shared__ cf32 tile[kTile * kTile];
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const long long per_array = static_cast<long long>(tiles_p) * tiles_q;
-    for (long long t = blockIdx.x; t < tiles; t += gridDim.x) {
+    for (long long t0 = blockIdx.x; t0 < tiles; t0 += gridDim.x) {
+        const long long t = gridDim.x == tiles ? xcd_grouped(t0, tiles, group) : t0;
         const long long b = t / per_array;
         const int rest = static_cast<int>(t - b * per_array);
         const int tq = rest / tiles_p;
@@ -200,8 +219,12 @@ void remap(const cf32* x, cf32* y, const Remap& r, bool transposed, hipStream_t 
         const int tiles_p = (r.y_cols - extra_p + kTile - 1) / kTile;
         const int tiles_q = (r.y_rows - extra_q + kTile - 1) / kTile;
         const long long tiles = static_cast<long long>(tiles_p) * tiles_q * r.batch;
+        // Output rows that do not start on 128-byte lines: runs of 8 consecutive tiles (the
+        // tiles of a band, then the next bands and arrays, which share lines at their edges) on
+        // one XCD each.
+        const int group = r.y_cols % 16 != 0 ? 8 : 1;
         hipLaunchKernelGGL(remap_tiles_kernel, dim3(blocks(tiles)), dim3(kTileThreads), 0, stream,
-                           x, y, r, tiles_p, tiles_q, tiles, extra_p, extra_q);
+                           x, y, r, tiles_p, tiles_q, tiles, extra_p, extra_q, group);
     } else {
         int lanes_log2 = 0;
         while (lanes_log2 < 6 && (1 << lanes_log2) < r.y_cols) {
