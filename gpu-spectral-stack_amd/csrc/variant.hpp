@@ -1116,7 +1116,8 @@ struct Fused2dDriver {
         // M = N2: complex rows of n2 values; 128 x 128 takes a 140 KB tile. With 128 rows, one
         // array per workgroup of 1024 lanes: 128 x 128 76.4 -> 71.7 us and 128 x 64 56.4 ->
         // 53.4 us over 2^24 points on MI355X against 512 lanes (64 x 128 unchanged; the real
-        // kernels at 128 x 128 measured 39 % slower with 1024).
+        // kernels at 128 x 128 measured 39 % slower with 1024, and still 3-6 % slower with one
+        // row pass, 8-value columns and 43-55 VGPRs, i.e. 8 waves per SIMD).
         using F = dev::Fused2d<N1, N2, R, Table, (N1 * N2 > 8192 ? 160 : 80),
                                (N1 >= 128 ? 1024 : 512)>;
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
