@@ -1391,8 +1391,11 @@ __global__ void __launch_bounds__(P::kThreads)
     };
     // The last pass of a transform (final output) also loads nontemporally: 1 point of the peak
     // faster for the inverse 2D and fft2_c2c column passes at 256 and 512 points, where the
-    // forward's first pass measured 1-2 points slower with it.
-    const bool nt = io.stream_out;
+    // forward's first pass measured 1-2 points slower with it. Not for tiles narrower than a
+    // cache line (C > 0): their neighbour tile, on the same XCD, reads the other half of each line
+    // from L2, which nontemporal loads do not leave there. Plain loads there: irfft2 1024^2
+    // 64.4 -> 57.0 us and fft2_c2c 1024^2 125.8 -> 103.2 us on MI355X (interleaved rounds).
+    const bool nt = io.stream_out && C == 0;
     cf32 val[StridedIo::steps<P>()];
     const long long offset = xcd_order<C>(blockIdx.x, gridDim.x);
     if (offset < tiles) {
