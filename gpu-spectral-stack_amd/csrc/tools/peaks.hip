@@ -110,7 +110,10 @@ __global__ void __launch_bounds__(Th) rows_copy_kernel(const f2v* __restrict__ i
 // Column tiles: arrays of Rows x Cols 8-byte values; workgroup b copies the tile of T neighbouring
 // columns x Rows rows (tile b mod Cols / T of array b / (Cols / T)), lane t taking column t mod T
 // and rows t / T + k Th / T: runs of T * 8 bytes, one per row, Cols * 8 bytes apart.
-template <int Rows, int Cols, int T, int Th, bool NT>
+// Side picks the layout of each end: 0 both row-major (the strided column pass in place), 1 the
+// output tile-major, 2 the input tile-major. Tile-major stores each tile's Rows x T values as one
+// contiguous block (array, tile, row, column in tile), so that end of the copy is contiguous.
+template <int Rows, int Cols, int T, int Th, bool NT, int Side = 0>
 __global__ void __launch_bounds__(Th) tiles_copy_kernel(const f2v* __restrict__ in, f2v* __restrict__ out)
 {
     constexpr int kTiles = Cols / T;
@@ -118,17 +121,57 @@ __global__ void __launch_bounds__(Th) tiles_copy_kernel(const f2v* __restrict__ 
     constexpr int kK = Rows / kStep;
     static_assert(Cols % T == 0 && Th % T == 0 && Rows % kStep == 0, "tile shape");
     const std::size_t array = blockIdx.x / kTiles;
-    const int col = static_cast<int>(blockIdx.x % kTiles) * T + static_cast<int>(threadIdx.x) % T;
+    const int tile = static_cast<int>(blockIdx.x % kTiles);
+    const int col = tile * T + static_cast<int>(threadIdx.x) % T;
     const int row = static_cast<int>(threadIdx.x) / T;
     const std::size_t base = array * Rows * Cols + col + static_cast<std::size_t>(row) * Cols;
+    const std::size_t tiled = array * Rows * Cols + static_cast<std::size_t>(tile) * Rows * T
+                              + threadIdx.x;
+    const std::size_t in_base = Side == 2 ? tiled : base;
+    const std::size_t out_base = Side == 1 ? tiled : base;
+    constexpr std::size_t kInStep = Side == 2 ? std::size_t(kStep) * T : std::size_t(kStep) * Cols;
+    constexpr std::size_t kOutStep = Side == 1 ? std::size_t(kStep) * T : std::size_t(kStep) * Cols;
     f2v v[kK];
 #pragma unroll
     for (int k = 0; k < kK; ++k) {
-        v[k] = load8<NT>(in + base + static_cast<std::size_t>(k) * kStep * Cols);
+        v[k] = load8<NT>(in + in_base + static_cast<std::size_t>(k) * kInStep);
     }
 #pragma unroll
     for (int k = 0; k < kK; ++k) {
-        store8<NT>(out + base + static_cast<std::size_t>(k) * kStep * Cols, v[k]);
+        store8<NT>(out + out_base + static_cast<std::size_t>(k) * kOutStep, v[k]);
+    }
+}
+
+// Whole rows against a tile-major array (tiles of T columns, as above): workgroup b copies G
+// consecutive rows of one array, a contiguous run of G * Cols values on the row-major side and,
+// on the tile-major side, one run of G * T values in each of the Cols / T tiles. ToTiles: the
+// row-major side is the input. Lanes walk the tile-major side in order, the other side in the
+// same order (a permuted copy: the floor of the two access patterns, not a layout change).
+template <int Rows, int Cols, int T, int G, int Th, bool ToTiles>
+__global__ void __launch_bounds__(Th) rows_tiles_copy_kernel(const f2v* __restrict__ in,
+                                                             f2v* __restrict__ out)
+{
+    constexpr int kTotal = G * Cols;
+    constexpr int kK = kTotal / Th;
+    static_assert(Cols % T == 0 && Rows % G == 0 && kTotal % Th == 0, "row group shape");
+    const std::size_t array = blockIdx.x / (Rows / G);
+    const int r0 = static_cast<int>(blockIdx.x % (Rows / G)) * G;
+    const std::size_t rows_base = array * Rows * Cols + static_cast<std::size_t>(r0) * Cols;
+    f2v v[kK];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) {
+        const int e = static_cast<int>(threadIdx.x) + k * Th;
+        const int j = e % T;
+        const int g = (e / T) % G;
+        const int tile = e / (T * G);
+        const std::size_t tiled = array * Rows * Cols + static_cast<std::size_t>(tile) * Rows * T
+                                  + static_cast<std::size_t>(r0 + g) * T + j;
+        v[k] = ToTiles ? in[rows_base + e] : in[tiled];
+        if (ToTiles) {
+            out[tiled] = v[k];
+        } else {
+            out[rows_base + e] = v[k];
+        }
     }
 }
 
@@ -195,6 +238,22 @@ void launch_tiles(std::size_t values, const f2v* in, f2v* out, hipStream_t s)
                        dim3(Th), 0, s, in, out);
 }
 
+template <int Rows, int Cols, int T, int Th, bool NT, int Side>
+void launch_tiles_side(std::size_t values, const f2v* in, f2v* out, hipStream_t s)
+{
+    hipLaunchKernelGGL((tiles_copy_kernel<Rows, Cols, T, Th, NT, Side>),
+                       dim3(static_cast<unsigned>(values / (static_cast<std::size_t>(Rows) * T))),
+                       dim3(Th), 0, s, in, out);
+}
+
+template <int Rows, int Cols, int T, int G, int Th, bool ToTiles>
+void launch_rows_tiles(std::size_t values, const f2v* in, f2v* out, hipStream_t s)
+{
+    hipLaunchKernelGGL((rows_tiles_copy_kernel<Rows, Cols, T, G, Th, ToTiles>),
+                       dim3(static_cast<unsigned>(values / (static_cast<std::size_t>(G) * Cols))),
+                       dim3(Th), 0, s, in, out);
+}
+
 constexpr std::size_t k2e24 = std::size_t(1) << 24;
 constexpr std::size_t k2e23 = std::size_t(1) << 23;
 
@@ -217,6 +276,16 @@ int run_patterns()
          [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<512, 256, 32, 1024, false>(k2e23, i, o, s); }, {}},
         {"tiles 64 x 512 of 512 x 256, plain", "512-byte runs", k2e23,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<512, 256, 64, 1024, false>(k2e23, i, o, s); }, {}},
+        {"tiles 16 x 512 of 512 x 256 in, tile-major out, plain", "column pass into a tile-major workspace", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles_side<512, 256, 16, 1024, false, 1>(k2e23, i, o, s); }, {}},
+        {"tile-major in, tiles 16 x 512 of 512 x 256 out, nontemporal", "column pass from a tile-major workspace", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles_side<512, 256, 16, 1024, true, 2>(k2e23, i, o, s); }, {}},
+        {"tile-major in (4-row runs, 512 B), rows out", "row-pair pass from a tile-major workspace", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_rows_tiles<512, 256, 16, 4, 256, false>(k2e23, i, o, s); }, {}},
+        {"tile-major in (16-row runs, 2 KB), rows out", "row-pair pass, 1024-lane workgroups", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_rows_tiles<512, 256, 16, 16, 1024, false>(k2e23, i, o, s); }, {}},
+        {"rows in, tile-major out (4-row runs, 512 B)", "row-pair pass into a tile-major workspace", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_rows_tiles<512, 256, 16, 4, 256, true>(k2e23, i, o, s); }, {}},
         {"tiles 8 x 1024 of 1024 x 1024, plain", "2^20-point C2C column pass (64-byte runs)", k2e24,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<1024, 1024, 8, 512, false>(k2e24, i, o, s); }, {}},
         {"tiles 16 x 1024 of 1024 x 1024, plain", "128-byte runs", k2e24,

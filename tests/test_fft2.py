@@ -174,8 +174,9 @@ def test_single_pass_rfft2_and_irfft2(rng, impl, n1, n2):
 # read as complex, then one pass over pairs of rows (k1, -k1). n1 = 1 and 2 make every row its own
 # partner; batches of 3 leave the last workgroup's pairs partly empty. The inverse takes random,
 # non-Hermitian spectra: columns 0 and n2/2 are symmetrized across the pair as numpy does.
+# 512-row shapes cover C3's column kernel from one 16-column tile per array (512 x 32) to 256.
 COLUMN_FIRST_SHAPES = [(1, 64), (2, 32), (8, 256), (32, 512), (256, 256), (512, 512), (2048, 64),
-                       (16, 4096), (4, 8192)]
+                       (16, 4096), (4, 8192), (512, 32), (512, 64), (512, 2048), (512, 8192)]
 STOCKHAM_IMPLS = [impl for impl in spectral.FFT_IMPLS if impl.startswith("stockham")]
 
 
