@@ -107,6 +107,35 @@ __global__ void __launch_bounds__(Th) rows_copy_kernel(const f2v* __restrict__ i
     }
 }
 
+// Uneven mixes: workgroup b reads Th * V contiguous values as rows_copy_kernel does and writes
+// Th of them (each lane the sum of its V), or the mirror (Expand: reads Th, writes each V times).
+// V = 16 is the byte mix of a pruned 2D transform keeping a sixteenth of its input (C4).
+template <int Th, int V, bool Expand>
+__global__ void __launch_bounds__(Th) mix_rows_kernel(const f2v* __restrict__ in, f2v* __restrict__ out)
+{
+    const std::size_t wide = static_cast<std::size_t>(blockIdx.x) * Th * V + threadIdx.x;
+    const std::size_t narrow = static_cast<std::size_t>(blockIdx.x) * Th + threadIdx.x;
+    if constexpr (Expand) {
+        const f2v v = in[narrow];
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            store8<true>(out + wide + static_cast<std::size_t>(k) * Th, v);
+        }
+    } else {
+        f2v v[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            v[k] = load8<false>(in + wide + static_cast<std::size_t>(k) * Th);
+        }
+        f2v sum = v[0];
+#pragma unroll
+        for (int k = 1; k < V; ++k) {
+            sum += v[k];
+        }
+        store8<true>(out + narrow, sum);
+    }
+}
+
 // Column tiles: arrays of Rows x Cols 8-byte values; workgroup b copies the tile of T neighbouring
 // columns x Rows rows (tile b mod Cols / T of array b / (Cols / T)), lane t taking column t mod T
 // and rows t / T + k Th / T: runs of T * 8 bytes, one per row, Cols * 8 bytes apart.
@@ -254,6 +283,13 @@ void launch_rows_tiles(std::size_t values, const f2v* in, f2v* out, hipStream_t 
                        dim3(Th), 0, s, in, out);
 }
 
+template <int Th, int V, bool Expand>
+void launch_mix(std::size_t wide_values, const f2v* in, f2v* out, hipStream_t s)
+{
+    hipLaunchKernelGGL((mix_rows_kernel<Th, V, Expand>),
+                       dim3(static_cast<unsigned>(wide_values / (Th * V))), dim3(Th), 0, s, in, out);
+}
+
 constexpr std::size_t k2e24 = std::size_t(1) << 24;
 constexpr std::size_t k2e23 = std::size_t(1) << 23;
 
@@ -268,6 +304,10 @@ int run_patterns()
          [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, true>(k2e23, i, o, s); }, {}},
         {"rows 16 KB chunks, plain", "C3 512^2 row-pair pass (2^23 values)", k2e23,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, false>(k2e23, i, o, s); }, {}},
+        {"rows, 16 B read per 1 B written", "C4 rfft2_modes: 128 MiB in, 8 MiB out", (k2e24 + k2e24 / 16) / 2,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 16, false>(k2e24, i, o, s); }, {}},
+        {"rows, 1 B read per 16 B written", "C4 irfft2_modes: 8 MiB in, 128 MiB out", (k2e24 + k2e24 / 16) / 2,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 16, true>(k2e24, i, o, s); }, {}},
         {"tiles 16 x 512 of 512 x 256, plain", "C3 512^2 column pass (128-byte runs)", k2e23,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<512, 256, 16, 1024, false>(k2e23, i, o, s); }, {}},
         {"tiles 16 x 512 of 512 x 256, nontemporal", "C3 512^2 column pass, nontemporal", k2e23,
