@@ -436,12 +436,15 @@ def test_mode_gather_and_scatter_edges(lib, rng, n1, w, m1, m2):
                                                      (4, 3, 4096), (31, 40, 5), (1000, 20, 2),
                                                      (32, 32, 3), (128, 65, 5), (65, 128, 5),
                                                      (257, 512, 2), (512, 257, 2), (65, 65, 3),
-                                                     (129, 193, 2), (33, 65, 3), (65, 40, 3)])
+                                                     (129, 193, 2), (33, 65, 3), (65, 40, 3),
+                                                     (193, 65, 3), (65, 193, 3), (193, 129, 2),
+                                                     (79, 129, 3), (80, 128, 2), (100, 100, 3)])
 def test_transpose_is_exact(lib, rng, rows, cols, batch):
     # Partial tiles on both axes, a single column or row, and a 1024 x 16384 matrix; arrays
     # with fewer than 32 rows or columns take the flat path (4 x 3: a 4 x 4 real transform's).
     # Sizes of 64k + 1 (a real spectrum's n/2 + 1) have their last row or column copied by the
-    # last full tile's workgroup, alone, with the other axis full or partial, and both at once.
+    # last full tile's workgroup, alone (128 x 65, 193 x 65, 65 x 193, 257 x 512), with the other
+    # axis full or partial, and both at once (65 x 65, 193 x 129, 129 x 193).
     x = (rng.standard_normal((batch, rows, cols)) + 1j * rng.standard_normal((batch, rows, cols)))
     xd = torch.from_numpy(x.astype(np.complex64)).cuda()
     yd = torch.empty(batch, cols, rows, dtype=torch.complex64, device="cuda")
