@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <stdexcept>
 #include <string>
@@ -61,5 +62,26 @@ inline int ilog2_host(long long n)
 }
 
 inline std::string str(long long v) { return std::to_string(v); }
+
+// Compute units of the current device, looked up once per device.
+inline int device_cus()
+{
+    int device = 0;
+    SPX_HIP_CHECK(hipGetDevice(&device));
+    constexpr int kDevices = 64;
+    static std::atomic<int> known[kDevices] = {};
+    if (device < kDevices) {
+        const int cus = known[device].load(std::memory_order_relaxed);
+        if (cus > 0) {
+            return cus;
+        }
+    }
+    int cus = 0;
+    SPX_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+    if (device < kDevices) {
+        known[device].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
+}
 
 }  // namespace spx

@@ -109,27 +109,6 @@ void dispatch_columns(int n, const Io& io, long long batch, hipStream_t stream)
     }
 }
 
-// Compute units of the current device, looked up once per device.
-inline int device_cus()
-{
-    int device = 0;
-    SPX_HIP_CHECK(hipGetDevice(&device));
-    constexpr int kDevices = 64;
-    static std::atomic<int> known[kDevices] = {};
-    if (device < kDevices) {
-        const int cus = known[device].load(std::memory_order_relaxed);
-        if (cus > 0) {
-            return cus;
-        }
-    }
-    int cus = 0;
-    SPX_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
-    if (device < kDevices) {
-        known[device].store(cus, std::memory_order_relaxed);
-    }
-    return cus;
-}
-
 // The persistent strided column kernel over as many workgroups as fit on the device at once.
 // Workgroups per CU depend only on the kernel and the architecture (gfx950 everywhere this
 // library runs), so the first query serves every device; the CU count is per device.
