@@ -22,7 +22,8 @@
 //   current tile's column reads and stores (bounded to 64 VGPRs, eight waves per SIMD). Against
 //   one tile per workgroup, three alternated rounds of the transpose method: 512^2 x 64
 //   100.2-100.6 -> 97.7-98.0 us (rfft2) and 95.0-95.4 -> 93.1-93.3 us (irfft2); 128^2 x 1024
-//   0.5 % faster.
+//   0.5 % faster. Two or three resident workgroups per CU, each with more tiles, ran the same
+//   (within 0.5 us).
 // * Not transposed: each output row is walked by a power-of-two group of lanes as wide as the row
 //   (up to a wave), so short rows (16 modes) still fill whole waves with several rows each. The
 //   row and column maps are evaluated per lane; no flat-index division per value.
