@@ -136,6 +136,7 @@ int spx_impl_get_info(int impl, spx_impl_info* out)
         out->max_c2c_n = i.max_c2c_n;
         out->max_real_n = i.max_real_n;
         out->real_needs_work = i.real_needs_work;
+        out->lazy_table = i.lazy_table;
     });
 }
 

@@ -108,6 +108,9 @@ struct FftImpl {
     // c2c with the caller's scratch for the sizes that need one (c2c_scratch_values), instead
     // of scratch allocated on the stream; nullptr when no size needs scratch.
     C2cWorkFn c2c_work;
+    // The first call on a device allocates a per-device table (twiddle_table), so the entry
+    // points that promise no allocation refuse this implementation.
+    bool lazy_table;
 };
 
 // Scratch values c2c_work needs for batch transforms of n points: n x batch beyond the

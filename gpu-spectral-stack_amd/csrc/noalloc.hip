@@ -50,14 +50,14 @@ cf32* scratch_on_current_device()
 void c2c_noalloc(const FftImpl& impl, const cf32* x, cf32* y, int n, int batch,
                  Direction direction, hipStream_t stream)
 {
-    if (impl.c2c_work == nullptr) {
-        impl.c2c(x, y, n, batch, direction, stream);  // no size of this implementation allocates
-        return;
-    }
-    if (impl.c2c_work == &c2c_work_stockham_r8_table) {
+    if (impl.lazy_table) {
         throw InvalidArgument("spx_c2c_noalloc: " + std::string(impl.name)
                               + " allocates its twiddle table on first use; use an "
                                 "implementation with computed twiddles");
+    }
+    if (impl.c2c_work == nullptr) {
+        impl.c2c(x, y, n, batch, direction, stream);  // no size of this implementation allocates
+        return;
     }
     if (!is_pow2(n) || n > impl.max_c2c_n || batch < 1) {
         // Rejected by the transform's own argument checks, before it would allocate anything.

@@ -9,20 +9,20 @@ namespace {
 
 const FftImpl kImpls[] = {
     {"naive", &c2c_naive, &r2c_naive, &c2r_naive, nullptr, nullptr, 1 << 30, 1 << 30, 1 << 30,
-     true, nullptr, nullptr, nullptr},
+     true, nullptr, nullptr, nullptr, false},
     {"stockham_r2", &c2c_stockham_r2, &r2c_stockham_r2, &c2r_stockham_r2, &columns_stockham_r2,
      &pruned_stockham_r2, kStockhamMaxN, kFourStepMaxN, 2 * kStockhamMaxN, false, &fused_stockham_r2,
-     &rf_stockham_r2, &c2c_work_stockham_r2},
+     &rf_stockham_r2, &c2c_work_stockham_r2, false},
     {"stockham_r4", &c2c_stockham_r4, &r2c_stockham_r4, &c2r_stockham_r4, &columns_stockham_r4,
      &pruned_stockham_r4, kStockhamMaxN, kFourStepMaxN, 2 * kStockhamMaxN, false, &fused_stockham_r4,
-     &rf_stockham_r4, &c2c_work_stockham_r4},
+     &rf_stockham_r4, &c2c_work_stockham_r4, false},
     {"stockham_r8", &c2c_stockham_r8, &r2c_stockham_r8, &c2r_stockham_r8, &columns_stockham_r8,
      &pruned_stockham_r8, kStockhamMaxN, kFourStepMaxN, 2 * kStockhamMaxN, false, &fused_stockham_r8,
-     &rf_stockham_r8, &c2c_work_stockham_r8},
+     &rf_stockham_r8, &c2c_work_stockham_r8, false},
     {"stockham_r8_table", &c2c_stockham_r8_table, &r2c_stockham_r8_table,
      &c2r_stockham_r8_table, &columns_stockham_r8_table, &pruned_stockham_r8_table,
      kStockhamMaxN, kFourStepMaxN, 2 * kStockhamMaxN, false, &fused_stockham_r8_table,
-     &rf_stockham_r8_table, &c2c_work_stockham_r8_table},
+     &rf_stockham_r8_table, &c2c_work_stockham_r8_table, true},
 };
 
 }  // namespace

@@ -212,14 +212,18 @@ __global__ void __launch_bounds__(kThreads)
     const Index stride = static_cast<Index>(gridDim.x) * kThreads;
     for (Index e = static_cast<Index>(blockIdx.x) * kThreads + threadIdx.x; e < total;
          e += stride) {
+        // The offset within an array stays in Index: one array may hold more than 2^31 values
+        // (16 x 2^28 fits in HBM). Its row and column each fit an int.
         const Index b = e / area;
-        const int rest = static_cast<int>(e - b * area);
-        const int q = rest / r.y_cols;
-        const int p = rest - q * r.y_cols;
+        const Index rest = e - b * area;
+        const Index q_wide = rest / static_cast<Index>(r.y_cols);
+        const int q = static_cast<int>(q_wide);
+        const int p = static_cast<int>(rest - q_wide * static_cast<Index>(r.y_cols));
         const int xr = r.rows(Transposed ? p : q);
         const int xc = r.cols(Transposed ? q : p);
         y[e] = (xr >= 0 && xc >= 0)
-                   ? x[static_cast<long long>(b) * r.x_array + xr * r.x_pitch + xc]
+                   ? x[static_cast<long long>(b) * r.x_array
+                       + static_cast<long long>(xr) * r.x_pitch + xc]
                    : zero();
     }
 }

@@ -1,15 +1,19 @@
 // spectral_bench: times every implementation of every operation of libspectral_hip.so on one
 // MI355X, next to rocFFT (through hipFFT), and writes one CSV row per (operation, implementation,
-// size, batch). The command line and the CSV schema are those of the reference's
-// csrc/tools/spectral_bench.cpp:48-60 and :185, so its result files and regression comparisons
-// (python/spectral/benchmark.py compare) work on these rows; the baseline row is "rocfft" where
+// size, batch). The flags and the first nine CSV columns are those of the reference's
+// csrc/tools/spectral_bench.cpp:48-60 and :185, so its result files and regression checks
+// (python -m spectral.benchmark compare) work on these rows; the baseline row is "rocfft" where
 // the reference has "cufft".
 //
 // What differs, for this GPU:
-// * Every row rotates over --rotate buffer sets (input, output), 3 by default. At the default
-//   2^24 points one set is 256 MiB, the size of MI355X's Infinity Cache, so three sets make every
-//   launch read data the previous launches evicted: the rates are HBM rates, not cache rates.
-// * The CSV carries one more column, pct_peak: gbps as a percentage of the 8 TB/s HBM peak.
+// * Every row rotates over --rotate buffer sets (input, output), 8 by default. At the default
+//   2^24 points a set's input is 64 MiB (real) to 128 MiB (complex), so the inputs in rotation
+//   total at least 512 MiB, twice MI355X's 256 MB Infinity Cache: a launch reads data that the
+//   launches since its set's last use have evicted, and the rates are HBM rates.
+// * Two more columns: pct_peak_datasheet, gbps as a percentage of the 8 TB/s HBM peak, and
+//   pct_peak_measured, of the copy ceiling measured at start-up (spx_scale streaming 1 GiB into
+//   another 1 GiB, the header says the figure) or given with --copy-peak.
+// * --impl takes a comma-separated list (e.g. rocfft,stockham_r8); --sizes takes powers of two.
 //
 // Each size runs batch = total / n transforms (2^24 points by default); 2D rows use n x n arrays,
 // batch = total / n^2. Pruned 2D rows keep m1 = m2 = max(1, n/8) modes; rocFFT has no pruned
@@ -18,8 +22,9 @@
 // events on one stream; the median per launch is reported, and a row whose rounds differ by
 // more than 5 % gets a warning on stderr.
 //
-//   spectral_bench [--op NAME] [--impl NAME] [--sizes LIST] [--total N] [--batches LIST]
-//                  [--warmup N] [--rounds N] [--iters N] [--rotate N] [--out FILE]
+//   spectral_bench [--op NAME] [--impl LIST] [--sizes LIST] [--total N] [--batches LIST]
+//                  [--warmup N] [--rounds N] [--iters N] [--rotate N] [--copy-peak GBPS]
+//                  [--out FILE]
 
 #include "spectral_hip.h"
 
@@ -27,6 +32,7 @@
 #include <hipfft/hipfft.h>
 
 #include <algorithm>
+#include <cerrno>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -35,7 +41,6 @@
 #include <functional>
 #include <iostream>
 #include <random>
-#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -47,18 +52,20 @@ constexpr double kUnstableSpread = 0.05;  // max / min - 1 above this gets a war
 
 const char* const kUsage =
     "usage: spectral_bench [options]\n"
-    "  --op NAME       all (default), fft_c2c, fft_r2c, fft_c2r, fft2_c2c, fft2_r2c,\n"
-    "                  fft2_c2r, rfft2_modes, irfft2_modes, scale, or ns_step\n"
-    "  --impl NAME     all (default), rocfft, ours (the scale kernel), or one of our FFTs\n"
-    "  --sizes LIST    comma-separated transform sizes (default: 2,4,...,4096)\n"
-    "  --total N       points per row; batch = total / n (default: 16777216)\n"
-    "  --batches LIST  comma-separated batch counts to run at every size instead of\n"
-    "                  total / n (rows whose points exceed --total are skipped)\n"
-    "  --warmup N      untimed launches (default: 3)\n"
-    "  --rounds N      timed measurements; the median is reported (default: 5)\n"
-    "  --iters N       launches per measurement (default: 20)\n"
-    "  --rotate N      buffer sets the launches rotate over (default: 3)\n"
-    "  --out FILE      write the CSV to FILE instead of standard output\n";
+    "  --op NAME         all (default), fft_c2c, fft_r2c, fft_c2r, fft2_c2c, fft2_r2c,\n"
+    "                    fft2_c2r, rfft2_modes, irfft2_modes, scale, or ns_step\n"
+    "  --impl LIST       all (default), or a comma-separated list of rocfft, ours (the scale\n"
+    "                    and ns_step kernels) and our FFTs\n"
+    "  --sizes LIST      comma-separated transform sizes, powers of two (default: 2,4,...,4096)\n"
+    "  --total N         points per row; batch = total / n (default: 16777216)\n"
+    "  --batches LIST    comma-separated batch counts to run at every size instead of\n"
+    "                    total / n (rows whose points exceed --total are skipped)\n"
+    "  --warmup N        untimed launches (default: 3)\n"
+    "  --rounds N        timed measurements; the median is reported (default: 5)\n"
+    "  --iters N         launches per measurement (default: 20)\n"
+    "  --rotate N        buffer sets the launches rotate over (default: 8)\n"
+    "  --copy-peak GBPS  the copy ceiling for pct_peak_measured (default: measured)\n"
+    "  --out FILE        write the CSV to FILE instead of standard output\n";
 
 void hip_check(hipError_t err, const char* what)
 {
@@ -84,46 +91,72 @@ void spx_check(int rc, const char* what)
 
 struct Options {
     std::string op = "all";
-    std::string impl = "all";
+    std::vector<std::string> impls;  // empty: all
     std::vector<long long> sizes;
     std::vector<long long> batches;
     long long total = 1LL << 24;
     int warmup = 3;
     int rounds = 5;
     int iters = 20;
-    int rotate = 3;
+    int rotate = 8;
+    double copy_peak = 0;  // GB/s; 0: measure
     std::string out;
 
-    bool wants(const std::string& name) const { return impl == "all" || impl == name; }
+    bool wants(const std::string& name) const
+    {
+        return impls.empty() || std::find(impls.begin(), impls.end(), name) != impls.end();
+    }
 };
 
-long long parse_int(const std::string& text, const std::string& flag, long long min_value)
+// A flag's value that cannot be used: the message names the flag, then the usage follows.
+struct FlagError : std::invalid_argument {
+    FlagError(const std::string& flag, const std::string& what)
+        : std::invalid_argument(flag + ": " + what + "\n" + kUsage)
+    {
+    }
+};
+
+std::vector<std::string> split_commas(const std::string& text)
 {
-    std::size_t used = 0;
-    long long value = 0;
-    try {
-        value = std::stoll(text, &used);
-    } catch (const std::exception&) {
-        used = 0;
+    std::vector<std::string> items;
+    std::size_t from = 0;
+    while (from <= text.size()) {
+        const std::size_t comma = std::min(text.find(',', from), text.size());
+        items.push_back(text.substr(from, comma - from));
+        from = comma + 1;
     }
-    if (used == 0 || used != text.size() || value < min_value) {
-        throw std::invalid_argument(flag + " needs an integer of at least "
-                                    + std::to_string(min_value) + ", got '" + text + "'\n"
-                                    + kUsage);
-    }
-    return value;
+    return items;
 }
 
-std::vector<long long> parse_list(const std::string& text, const std::string& flag)
+// A whole decimal integer >= lowest (strtoll must consume every character).
+long long to_count(const std::string& text, const std::string& flag, long long lowest)
+{
+    if (text.empty()) {
+        throw FlagError(flag, "empty value");
+    }
+    errno = 0;
+    char* end = nullptr;
+    const long long v = std::strtoll(text.c_str(), &end, 10);
+    if (errno != 0 || end != text.c_str() + text.size()) {
+        throw FlagError(flag, "'" + text + "' is not an integer");
+    }
+    if (v < lowest) {
+        throw FlagError(flag, "'" + text + "' is below the least allowed value "
+                                  + std::to_string(lowest));
+    }
+    return v;
+}
+
+std::vector<long long> to_counts(const std::string& text, const std::string& flag,
+                                 bool powers_of_two)
 {
     std::vector<long long> values;
-    std::stringstream stream(text);
-    std::string item;
-    while (std::getline(stream, item, ',')) {
-        values.push_back(parse_int(item, flag, 1));
-    }
-    if (values.empty()) {
-        throw std::invalid_argument(flag + " needs at least one value\n" + kUsage);
+    for (const std::string& item : split_commas(text)) {
+        const long long v = to_count(item, flag, 1);
+        if (powers_of_two && (v & (v - 1)) != 0) {
+            throw FlagError(flag, "'" + item + "' is not a power of two");
+        }
+        values.push_back(v);
     }
     return values;
 }
@@ -139,43 +172,53 @@ Options parse_options(int argc, char** argv)
             std::exit(0);
         }
         if (i + 1 >= argc) {
-            throw std::invalid_argument("missing value after " + flag + "\n" + kUsage);
+            throw FlagError(flag, "needs a value");
         }
         const std::string v = argv[++i];
         if (flag == "--op") {
+            static const char* const ops[] = {
+                "all",      "fft_c2c",     "fft_r2c",      "fft_c2r", "fft2_c2c", "fft2_r2c",
+                "fft2_c2r", "rfft2_modes", "irfft2_modes", "scale",   "ns_step"};
+            if (std::find(std::begin(ops), std::end(ops), v) == std::end(ops)) {
+                throw FlagError(flag, "unknown operation '" + v + "'");
+            }
             o.op = v;
         } else if (flag == "--impl") {
-            o.impl = v;
+            o.impls.clear();
+            if (v != "all") {
+                for (const std::string& name : split_commas(v)) {
+                    if (name != "rocfft" && name != "ours" && spx_impl_find(name.c_str()) < 0) {
+                        throw FlagError(flag, "unknown implementation '" + name
+                                                  + "' (our FFTs: " + spx_impl_names() + ")");
+                    }
+                    o.impls.push_back(name);
+                }
+            }
         } else if (flag == "--sizes") {
-            o.sizes = parse_list(v, flag);
+            o.sizes = to_counts(v, flag, true);
         } else if (flag == "--batches") {
-            o.batches = parse_list(v, flag);
+            o.batches = to_counts(v, flag, false);
         } else if (flag == "--total") {
-            o.total = parse_int(v, flag, 1);
+            o.total = to_count(v, flag, 1);
         } else if (flag == "--warmup") {
-            o.warmup = static_cast<int>(parse_int(v, flag, 0));
+            o.warmup = static_cast<int>(std::min(to_count(v, flag, 0), 1LL << 20));
         } else if (flag == "--rounds") {
-            o.rounds = static_cast<int>(parse_int(v, flag, 1));
+            o.rounds = static_cast<int>(std::min(to_count(v, flag, 1), 1LL << 20));
         } else if (flag == "--iters") {
-            o.iters = static_cast<int>(parse_int(v, flag, 1));
+            o.iters = static_cast<int>(std::min(to_count(v, flag, 1), 1LL << 20));
         } else if (flag == "--rotate") {
-            o.rotate = static_cast<int>(parse_int(v, flag, 1));
+            o.rotate = static_cast<int>(std::min(to_count(v, flag, 1), 64LL));
+        } else if (flag == "--copy-peak") {
+            char* end = nullptr;
+            o.copy_peak = std::strtod(v.c_str(), &end);
+            if (v.empty() || end != v.c_str() + v.size() || !(o.copy_peak > 0)) {
+                throw FlagError(flag, "'" + v + "' is not a positive rate in GB/s");
+            }
         } else if (flag == "--out") {
             o.out = v;
         } else {
-            throw std::invalid_argument("unknown option " + flag + "\n" + kUsage);
+            throw FlagError(flag, "unknown option");
         }
-    }
-    static const char* const ops[] = {"all",      "fft_c2c",  "fft_r2c",     "fft_c2r",
-                                      "fft2_c2c", "fft2_r2c", "fft2_c2r",    "rfft2_modes",
-                                      "irfft2_modes", "scale",    "ns_step"};
-    if (std::none_of(std::begin(ops), std::end(ops), [&](const char* s) { return o.op == s; })) {
-        throw std::invalid_argument("unknown --op " + o.op + "\n" + kUsage);
-    }
-    if (o.impl != "all" && o.impl != "rocfft" && o.impl != "ours"
-        && spx_impl_find(o.impl.c_str()) < 0) {
-        throw std::invalid_argument("unknown --impl " + o.impl + " (our FFTs: " + spx_impl_names()
-                                    + ")");
     }
     if (o.sizes.empty()) {
         for (long long n = 2; n <= 4096; n *= 2) {
@@ -261,16 +304,17 @@ Work modes_work(double n1, double n2, double m1, double m2, double batch)
 // --- output ---------------------------------------------------------------------------------
 
 int unstable_rows = 0;
+double copy_peak_gbps = 0;  // the measured (or given) copy ceiling of pct_peak_measured
 
 void write_row(std::ostream& os, const std::string& op, const std::string& impl, long long n,
                long long batch, const Timing& t, const Work& w, bool progress)
 {
     const double gflops = w.flops / (t.median_ms * 1e6);
     const double gbps = w.bytes / (t.median_ms * 1e6);
-    char line[320];
-    std::snprintf(line, sizeof line, "%s,%s,%lld,%lld,%.6f,%.6f,%.6f,%.1f,%.1f,%.1f\n",
+    char line[384];
+    std::snprintf(line, sizeof line, "%s,%s,%lld,%lld,%.6f,%.6f,%.6f,%.1f,%.1f,%.1f,%.1f\n",
                   op.c_str(), impl.c_str(), n, batch, t.median_ms, t.min_ms, t.max_ms, gflops,
-                  gbps, 100.0 * gbps / kPeakGbps);
+                  gbps, 100.0 * gbps / kPeakGbps, 100.0 * gbps / copy_peak_gbps);
     os << line << std::flush;
     if (progress) {
         std::fprintf(stderr, "%-12s %-22s n=%-6lld batch=%-9lld %9.4f ms %8.1f GB/s %5.1f %%\n",
@@ -284,7 +328,7 @@ void write_row(std::ostream& os, const std::string& op, const std::string& impl,
     }
 }
 
-void write_header(std::ostream& os, const Options& o)
+void write_header(std::ostream& os, const Options& o, bool measured)
 {
     int device = 0;
     hip_check(hipGetDevice(&device), "hipGetDevice");
@@ -296,13 +340,19 @@ void write_header(std::ostream& os, const Options& o)
     hip_check(hipDriverGetVersion(&driver), "hipDriverGetVersion");
     int fftver = 0;
     fft_check(hipfftGetVersion(&fftver), "hipfftGetVersion");
+    char peak[160];
+    std::snprintf(peak, sizeof peak, "%.1f GB/s (%s)", copy_peak_gbps,
+                  measured ? "spx_scale, 1 GiB -> 1 GiB, median of 5 rounds" : "--copy-peak");
     os << "# device: " << prop.name << " (" << prop.gcnArchName << "), "
        << prop.multiProcessorCount << " CUs\n"
        << "# HIP runtime " << runtime << ", driver " << driver << ", hipFFT " << fftver << '\n'
        << "# timing: " << o.warmup << " warm-up launches, then the median over " << o.rounds
        << " rounds of " << o.iters << " launches rotating over " << o.rotate
-       << " buffer sets; times are per launch; pct_peak is gbps / 8000\n"
-       << "op,impl,n,batch,time_ms,min_ms,max_ms,gflops,gbps,pct_peak\n";
+       << " buffer sets; times are per launch\n"
+       << "# pct_peak_datasheet = gbps / 8000; pct_peak_measured = gbps / copy ceiling " << peak
+       << '\n'
+       << "op,impl,n,batch,time_ms,min_ms,max_ms,gflops,gbps,pct_peak_datasheet,"
+          "pct_peak_measured\n";
 }
 
 // --- buffers --------------------------------------------------------------------------------
@@ -312,22 +362,24 @@ struct Buffers {
     std::vector<void*> y;  // outputs
     std::size_t bytes = 0;
 
+    // Every set holds the same standard-normal values: the caches see distinct addresses,
+    // whatever the values.
     Buffers(int sets, std::size_t nbytes) : bytes(nbytes)
     {
         std::mt19937 gen(12345);
         std::normal_distribution<float> normal(0.0f, 1.0f);
         std::vector<float> host(nbytes / sizeof(float));
+        for (float& v : host) {
+            v = normal(gen);
+        }
         for (int s = 0; s < sets; ++s) {
-            for (float& v : host) {
-                v = normal(gen);
-            }
             void* a = nullptr;
             void* b = nullptr;
             hip_check(hipMalloc(&a, nbytes), "hipMalloc");
-            hip_check(hipMalloc(&b, nbytes), "hipMalloc");
-            hip_check(hipMemcpy(a, host.data(), nbytes, hipMemcpyHostToDevice), "hipMemcpy");
             x.push_back(a);
+            hip_check(hipMalloc(&b, nbytes), "hipMalloc");
             y.push_back(b);
+            hip_check(hipMemcpy(a, host.data(), nbytes, hipMemcpyHostToDevice), "hipMemcpy");
         }
     }
     ~Buffers()
@@ -355,6 +407,25 @@ struct Scratch {
     Scratch(const Scratch&) = delete;
     Scratch& operator=(const Scratch&) = delete;
 };
+
+// The copy ceiling: spx_scale (one dwordx4 load and store per lane) streaming 1 GiB into another
+// 1 GiB, 8 times the Infinity Cache, so each launch reads HBM. Bytes: both sides.
+double measure_copy_peak(hipStream_t stream)
+{
+    constexpr std::size_t kValues = std::size_t(1) << 27;  // cf32: 1 GiB
+    Scratch src(kValues * 8);
+    Scratch dst(kValues * 8);
+    hip_check(hipMemsetAsync(src.p, 0, kValues * 8, stream), "hipMemsetAsync");
+    Options copy;
+    copy.warmup = 2;
+    copy.rounds = 5;
+    copy.iters = 5;
+    copy.rotate = 1;
+    const Timing t = time_launches(
+        [&](int, hipStream_t st) { spx_check(spx_scale(src.p, dst.p, kValues, 1.0f, st), "scale"); },
+        stream, copy);
+    return 2.0 * kValues * 8 / (t.median_ms * 1e6);
+}
 
 struct Plan {
     hipfftHandle h{};
@@ -727,7 +798,8 @@ int main(int argc, char** argv)
         }
         std::ostream& os = o.out.empty() ? std::cout : file;
         const bool progress = !o.out.empty();
-        write_header(os, o);
+        copy_peak_gbps = o.copy_peak > 0 ? o.copy_peak : measure_copy_peak(stream);
+        write_header(os, o, !(o.copy_peak > 0));
         auto want = [&](const char* op) { return o.op == "all" || o.op == op; };
         if (want("fft_c2c")) {
             bench_c2c(o, buffers, stream, os, progress);

@@ -53,6 +53,8 @@ typedef struct spx_impl_info {
     int max_c2c_n;        /* largest 1D complex transform */
     int max_real_n;       /* largest real transform */
     int real_needs_work;  /* r2c / c2r need the `work` buffer */
+    int lazy_table;       /* the first call on a device allocates a table (no reference field:
+                             spx_c2c_noalloc refuses these) */
 } spx_impl_info;
 
 /* --- registry: registry.hpp:28-62 (kFftImpls, find_impl, impl_names), ops.cpp:422-443 ------ */

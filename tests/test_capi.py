@@ -50,7 +50,7 @@ class Info(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("has_columns", ctypes.c_int),
                 ("has_pruned", ctypes.c_int), ("max_n", ctypes.c_int),
                 ("max_c2c_n", ctypes.c_int), ("max_real_n", ctypes.c_int),
-                ("real_needs_work", ctypes.c_int)]
+                ("real_needs_work", ctypes.c_int), ("lazy_table", ctypes.c_int)]
 
 
 def test_registry_rows(lib):
@@ -68,6 +68,11 @@ def test_registry_rows(lib):
     assert lib.spx_impl_get_info(3, ctypes.byref(info)) == SPX_OK
     assert (info.has_columns, info.has_pruned, info.max_n, info.max_c2c_n, info.max_real_n,
             info.real_needs_work) == (1, 1, 4096, 1 << 24, 8192, 0)
+    tables = []
+    for i in range(lib.spx_impl_count()):
+        assert lib.spx_impl_get_info(i, ctypes.byref(info)) == SPX_OK
+        tables.append(info.lazy_table)
+    assert tables == [0, 0, 0, 0, 1]  # only stockham_r8_table builds a table on first use
     assert lib.spx_impl_get_info(9, ctypes.byref(info)) == SPX_EINVAL
 
 
@@ -496,8 +501,17 @@ def test_noalloc_c2c_rejects_what_its_static_scratch_cannot_hold(lib):
     assert lib.spx_c2c_noalloc(3, p, q, 1 << 20, 5, 0, None) == SPX_EINVAL
     assert "split the batch" in _last(lib)
     assert lib.spx_c2c_noalloc(3, p, q, 1 << 24, 1, 0, None) == SPX_EINVAL
-    assert lib.spx_c2c_noalloc(4, p, q, 1 << 20, 1, 0, None) == SPX_EINVAL
-    assert "twiddle table" in _last(lib)
+    info = Info()
+    lazy = []
+    for impl in range(lib.spx_impl_count()):
+        assert lib.spx_impl_get_info(impl, ctypes.byref(info)) == SPX_OK
+        if info.lazy_table:
+            lazy.append(impl)
+    assert lazy, "the registry has a table variant"
+    for impl in lazy:  # refused at every size, before the table could be built
+        for n, batch in [(1 << 20, 1), (1024, 8), (2, 1)]:
+            assert lib.spx_c2c_noalloc(impl, p, q, n, batch, 0, None) == SPX_EINVAL
+            assert "twiddle table" in _last(lib)
     assert lib.spx_c2c_noalloc(3, p, q, 3 << 20, 1, 0, None) == SPX_EINVAL
     assert "power of two" in _last(lib)
     assert lib.spx_c2c_noalloc(3, p, q, 1 << 20, 0, 0, None) == SPX_EINVAL

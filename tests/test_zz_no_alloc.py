@@ -56,3 +56,45 @@ def test_noalloc_matches_c2c_on_calls_in_a_row(lib, rng):
             assert torch.equal(y_static, y_alloc), (n, batch, inverse)
         forward = _both(lib, x, n, batch, 0)[1]
         assert_transform_close(forward.cpu().numpy()[:1], ref.fft(x_host[:1]), n)
+
+
+def _hip_runtime() -> ctypes.CDLL:
+    # The HIP runtime this process already mapped: the one the library and PyTorch call.
+    for line in Path("/proc/self/maps").read_text().splitlines():
+        if "libamdhip64.so" in line.split()[-1]:
+            return ctypes.CDLL(line.split()[-1])
+    return ctypes.CDLL("libamdhip64.so")
+
+
+USED_MEM_HIGH = 8  # hipMemPoolAttrUsedMemHigh
+
+
+def test_noalloc_takes_nothing_from_the_stream_ordered_pool(lib, rng):
+    # spx_c2c's large transforms take their scratch from the device's default pool in stream
+    # order (hipMallocAsync, which is also legal under graph capture), so a noalloc that fell
+    # back to it would still match spx_c2c bit for bit. The pool's high-water mark of memory in
+    # use tells them apart: reset to zero, it must stay zero across noalloc calls and rise for
+    # the same transforms through spx_c2c.
+    hip = _hip_runtime()
+    pool = ctypes.c_void_p()
+    assert hip.hipDeviceGetDefaultMemPool(ctypes.byref(pool), torch.cuda.current_device()) == 0
+    high = ctypes.c_uint64()
+
+    def reset_and_run(entry, cases):
+        zero = ctypes.c_uint64(0)
+        torch.cuda.synchronize()
+        assert hip.hipMemPoolSetAttribute(pool, USED_MEM_HIGH, ctypes.byref(zero)) == 0
+        for x, y, n, batch in cases:
+            assert entry(STOCKHAM_R8, _ptr(x), _ptr(y), n, batch, 0, None) == 0, \
+                lib.spx_last_error().decode()
+        torch.cuda.synchronize()
+        assert hip.hipMemPoolGetAttribute(pool, USED_MEM_HIGH, ctypes.byref(high)) == 0
+        return high.value
+
+    cases = []
+    for n, batch in [(1 << 22, 1), (1 << 20, 4)]:
+        x = torch.from_numpy(random_complex(rng, (batch, n))).cuda()
+        cases.append((x, torch.empty_like(x), n, batch))
+    assert reset_and_run(lib.spx_c2c_noalloc, cases) == 0
+    assert reset_and_run(lib.spx_c2c, cases) >= (1 << 22) * 8  # the control does use the pool
+    assert reset_and_run(lib.spx_c2c_noalloc, cases) == 0
