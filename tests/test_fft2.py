@@ -1,5 +1,9 @@
-"""2D transforms against the float64 oracle (reference tests/test_fft2.py): every implementation
-with the transpose method, and the ones with a strided column kernel with that method too."""
+"""spectral.fft2 / rfft2 / irfft2 on the GPU (reference tests/test_fft2.py covers the same
+ground): parity with the float64 oracle for every implementation with the transpose column
+method and every Stockham implementation with the strided one, in both directions, over square,
+flat, tall and BASELINE C3 shapes; the inverse's reading of a non-Hermitian spectrum; round trips;
+batch layouts; `columns="auto"`; and the rejections with the reference's messages. Then the
+shapes of this stack's own single-pass, column-first and long-column kernels."""
 
 import numpy as np
 import pytest
@@ -17,6 +21,7 @@ METHODS = [(impl, "transpose") for impl in spectral.FFT_IMPLS] + [
     (impl, "strided") for impl in STOCKHAM
 ]
 METHOD_IDS = [f"{impl}-{cols}" for impl, cols in METHODS]
+DIRECTIONS = ["forward", "inverse"]
 
 # (1024, 8) and (1024, 16): 1024-point strided columns, the persistent kernel in XCD order.
 SHAPES = [(1, 8), (8, 1), (2, 2), (16, 16), (64, 32), (8, 256), (256, 8), (4096, 4), (4, 4096),
@@ -26,127 +31,128 @@ REAL_SHAPES = [(1, 8), (8, 2), (16, 16), (64, 32), (8, 256), (256, 8), (4096, 4)
                (128, 128), (512, 512), (1024, 16), (64, 1024), (128, 512)]
 
 
-def cuda(x: np.ndarray) -> torch.Tensor:
+def dev(x: np.ndarray) -> torch.Tensor:
     return torch.from_numpy(x).cuda()
 
 
+def close_2d(actual, expected, n1: int, n2: int, *, passes: int = 1) -> None:
+    """Within `passes` transforms' tolerance for n1 * n2 points, per array."""
+    n = n1 * n2
+    assert_transform_close(actual, expected, n, axes=AXES, tol=passes * fft_tolerance(n))
+
+
+@pytest.mark.parametrize("direction", DIRECTIONS)
 @pytest.mark.parametrize(("impl", "columns"), METHODS, ids=METHOD_IDS)
 @pytest.mark.parametrize(("n1", "n2"), SHAPES)
-def test_fft2_matches_the_oracle(rng, impl, columns, n1, n2):
+def test_complex_2d_parity(rng, n1, n2, impl, columns, direction):
     x = random_complex(rng, (3, n1, n2))
-    y = spectral.fft2(cuda(x), impl=impl, columns=columns)
-    assert_transform_close(y, ref.fft2(x), n1 * n2, axes=AXES)
+    inverse = direction == "inverse"
+    y = spectral.fft2(dev(x), inverse=inverse, impl=impl, columns=columns)
+    close_2d(y, ref.ifft2(x) if inverse else ref.fft2(x), n1, n2)
 
 
-@pytest.mark.parametrize(("impl", "columns"), METHODS, ids=METHOD_IDS)
-@pytest.mark.parametrize(("n1", "n2"), SHAPES)
-def test_ifft2_matches_the_oracle(rng, impl, columns, n1, n2):
-    x = random_complex(rng, (3, n1, n2))
-    y = spectral.fft2(cuda(x), inverse=True, impl=impl, columns=columns)
-    assert_transform_close(y, ref.ifft2(x), n1 * n2, axes=AXES)
-
-
+@pytest.mark.parametrize("direction", DIRECTIONS)
 @pytest.mark.parametrize(("impl", "columns"), METHODS, ids=METHOD_IDS)
 @pytest.mark.parametrize(("n1", "n2"), REAL_SHAPES)
-def test_rfft2_matches_the_oracle(rng, impl, columns, n1, n2):
-    x = random_real(rng, (3, n1, n2))
-    y = spectral.rfft2(cuda(x), impl=impl, columns=columns)
-    assert y.shape == (3, n1, n2 // 2 + 1)
-    assert_transform_close(y, ref.rfft2(x), n1 * n2, axes=AXES)
+def test_real_2d_parity(rng, n1, n2, impl, columns, direction):
+    field = random_real(rng, (3, n1, n2))
+    if direction == "forward":
+        y = spectral.rfft2(dev(field), impl=impl, columns=columns)
+        assert tuple(y.shape) == (3, n1, n2 // 2 + 1)
+        close_2d(y, ref.rfft2(field), n1, n2)
+    else:
+        half = ref.rfft2(field).astype(np.complex64)
+        y = spectral.irfft2(dev(half), n2, impl=impl, columns=columns)
+        assert tuple(y.shape) == (3, n1, n2)
+        close_2d(y, ref.irfft2(half, (n1, n2)), n1, n2)
 
 
 @pytest.mark.parametrize(("impl", "columns"), METHODS, ids=METHOD_IDS)
-@pytest.mark.parametrize(("n1", "n2"), REAL_SHAPES)
-def test_irfft2_matches_the_oracle(rng, impl, columns, n1, n2):
-    spectrum = ref.rfft2(random_real(rng, (3, n1, n2))).astype(np.complex64)
-    y = spectral.irfft2(cuda(spectrum), n2, impl=impl, columns=columns)
-    assert y.shape == (3, n1, n2)
-    assert_transform_close(y, ref.irfft2(spectrum, (n1, n2)), n1 * n2, axes=AXES)
+def test_inverse_reads_a_non_hermitian_half_spectrum_as_numpy_does(rng, impl, columns):
+    # The inverse is defined as complex inverses down the columns, then real inverses along the
+    # rows that ignore the imaginary parts of bins 0 and n2/2; written out here in float64.
+    half = random_complex(rng, (2, 16, 9))
+    expected = np.fft.irfft(np.fft.ifft(half.astype(np.complex128), axis=-2), n=16, axis=-1)
+    close_2d(spectral.irfft2(dev(half), 16, impl=impl, columns=columns), expected, 16, 16)
+
+
+@pytest.mark.parametrize("kind", ["complex", "real"])
+@pytest.mark.parametrize(("impl", "columns"), METHODS, ids=METHOD_IDS)
+def test_2d_round_trip(rng, impl, columns, kind):
+    if kind == "complex":
+        x = dev(random_complex(rng, (2, 32, 64)))
+        there = spectral.fft2(x, impl=impl, columns=columns)
+        back = spectral.fft2(there, inverse=True, impl=impl, columns=columns)
+    else:
+        x = dev(random_real(rng, (2, 32, 64)))
+        back = spectral.irfft2(spectral.rfft2(x, impl=impl, columns=columns), 64, impl=impl)
+    close_2d(back, x, 32, 64, passes=2)
 
 
 @pytest.mark.parametrize(("impl", "columns"), METHODS, ids=METHOD_IDS)
-def test_irfft2_of_a_non_hermitian_spectrum_matches_torch(rng, impl, columns):
-    spectrum = random_complex(rng, (2, 16, 9))
-    expected = torch.fft.irfft2(torch.from_numpy(spectrum).to(torch.complex128), s=(16, 16))
-    y = spectral.irfft2(cuda(spectrum), 16, impl=impl, columns=columns)
-    assert_transform_close(y, expected.numpy(), 256, axes=AXES)
+def test_arrays_spread_over_several_leading_dimensions(rng, impl, columns):
+    # 300 arrays of 8 x 16: one workgroup's column group spans several arrays.
+    field = random_real(rng, (2, 3, 50, 8, 16))
+    y = spectral.rfft2(dev(field), impl=impl, columns=columns)
+    assert tuple(y.shape) == (2, 3, 50, 8, 9)
+    close_2d(y, ref.rfft2(field), 8, 16)
 
 
 @pytest.mark.parametrize(("impl", "columns"), METHODS, ids=METHOD_IDS)
-def test_round_trips(rng, impl, columns):
-    x = cuda(random_complex(rng, (2, 32, 64)))
-    back = spectral.fft2(
-        spectral.fft2(x, impl=impl, columns=columns), inverse=True, impl=impl, columns=columns
-    )
-    assert_transform_close(back, x, 32 * 64, axes=AXES, tol=2 * fft_tolerance(32 * 64))
-    r = cuda(random_real(rng, (2, 32, 64)))
-    back = spectral.irfft2(spectral.rfft2(r, impl=impl, columns=columns), 64, impl=impl)
-    assert_transform_close(back, r, 32 * 64, axes=AXES, tol=2 * fft_tolerance(32 * 64))
+def test_permuted_view_is_transformed_as_its_values(rng, impl, columns):
+    view = dev(random_complex(rng, (16, 32, 3))).permute(2, 0, 1)
+    assert not view.is_contiguous()
+    close_2d(spectral.fft2(view, impl=impl, columns=columns), ref.fft2(view.cpu().numpy()),
+             16, 32)
 
 
-@pytest.mark.parametrize(("impl", "columns"), METHODS, ids=METHOD_IDS)
-def test_many_arrays_and_leading_dimensions(rng, impl, columns):
-    # 300 arrays of 8 x 16: column groups of one workgroup straddle arrays.
-    x = random_real(rng, (2, 3, 50, 8, 16))
-    y = spectral.rfft2(cuda(x), impl=impl, columns=columns)
-    assert y.shape == (2, 3, 50, 8, 9)
-    assert_transform_close(y, ref.rfft2(x), 128, axes=AXES)
+def test_auto_columns_is_strided_where_a_column_kernel_exists(rng):
+    # The same kernels in the same order: equal bits, not merely close values.
+    field = dev(random_real(rng, (4, 32, 32)))
+    for impl in spectral.FFT_IMPLS:
+        method = "strided" if impl in STOCKHAM else "transpose"
+        assert torch.equal(spectral.rfft2(field, impl=impl),
+                           spectral.rfft2(field, impl=impl, columns=method)), impl
 
 
-@pytest.mark.parametrize(("impl", "columns"), METHODS, ids=METHOD_IDS)
-def test_non_contiguous_input(rng, impl, columns):
-    x = cuda(random_complex(rng, (16, 32, 3))).permute(2, 0, 1)
-    assert not x.is_contiguous()
-    y = spectral.fft2(x, impl=impl, columns=columns)
-    assert_transform_close(y, ref.fft2(x.cpu().numpy()), 16 * 32, axes=AXES)
+@pytest.mark.parametrize("op", ["rfft2", "fft2", "irfft2"])
+def test_no_arrays_give_an_empty_result(op):
+    if op == "rfft2":
+        shape = spectral.rfft2(torch.zeros(0, 4, 8, device="cuda")).shape
+        assert tuple(shape) == (0, 4, 5)
+    elif op == "fft2":
+        shape = spectral.fft2(torch.zeros(0, 4, 8, dtype=torch.complex64, device="cuda")).shape
+        assert tuple(shape) == (0, 4, 8)
+    else:
+        half = torch.zeros(0, 4, 5, dtype=torch.complex64, device="cuda")
+        assert tuple(spectral.irfft2(half, 8).shape) == (0, 4, 8)
 
 
-def test_auto_picks_strided_when_available(rng):
-    x = cuda(random_real(rng, (4, 32, 32)))
-    for impl in STOCKHAM:
-        auto = spectral.rfft2(x, impl=impl)
-        assert torch.equal(auto, spectral.rfft2(x, impl=impl, columns="strided"))
-    naive = spectral.rfft2(x, impl="naive")
-    assert torch.equal(naive, spectral.rfft2(x, impl="naive", columns="transpose"))
+# --- rejections (the reference's messages) ---------------------------------------------------
+
+def _complex(*shape) -> torch.Tensor:
+    return torch.zeros(*shape, dtype=torch.complex64, device="cuda")
 
 
-def test_empty_input_gives_empty_output():
-    x = torch.zeros(0, 4, 8, device="cuda")
-    assert spectral.rfft2(x).shape == (0, 4, 5)
-    assert spectral.fft2(x.to(torch.complex64)).shape == (0, 4, 8)
-    empty = torch.zeros(0, 4, 5, dtype=torch.complex64, device="cuda")
-    assert spectral.irfft2(empty, 8).shape == (0, 4, 8)
-
-
-def test_rejects_strided_without_a_column_kernel():
-    x = torch.zeros(4, 8, dtype=torch.complex64, device="cuda")
-    with pytest.raises(RuntimeError, match="no strided column kernel"):
-        spectral.fft2(x, impl="naive", columns="strided")
-
-
-def test_rejects_an_unknown_column_method():
-    x = torch.zeros(4, 8, dtype=torch.complex64, device="cuda")
-    with pytest.raises(RuntimeError, match="columns must be"):
-        spectral.fft2(x, impl="naive", columns="sideways")
+@pytest.mark.parametrize(("call", "error", "message"), [
+    (lambda: spectral.fft2(_complex(4, 8), impl="naive", columns="strided"), RuntimeError,
+     "no strided column kernel"),
+    (lambda: spectral.fft2(_complex(4, 8), impl="naive", columns="sideways"), RuntimeError,
+     "columns must be"),
+    (lambda: spectral.rfft2(torch.zeros(8, device="cuda")), RuntimeError,
+     "at least two dimensions"),
+    (lambda: spectral.irfft2(_complex(4, 8), 8), RuntimeError, r"n2/2 \+ 1 = 5 input columns"),
+], ids=["strided-without-kernel", "unknown-method", "one-dimension", "spectrum-width"])
+def test_bad_2d_requests_are_refused(call, error, message):
+    with pytest.raises(error, match=message):
+        call()
 
 
 @pytest.mark.parametrize("impl", STOCKHAM)
-def test_rejects_columns_longer_than_the_kernel_supports(impl):
-    # Raised by the driver as an invalid argument: ValueError, as in the reference.
-    x = torch.zeros(8192, 2, dtype=torch.complex64, device="cuda")
+def test_columns_past_the_kernel_limit_are_a_value_error(impl):
+    # An invalid argument of the driver: ValueError, as the reference's std::invalid_argument.
     with pytest.raises(ValueError, match="n1 to be a power of two up to 4096"):
-        spectral.fft2(x, impl=impl)
-
-
-def test_rejects_one_dimensional_input():
-    with pytest.raises(RuntimeError, match="at least two dimensions"):
-        spectral.rfft2(torch.zeros(8, device="cuda"))
-
-
-def test_rejects_a_spectrum_of_the_wrong_width():
-    x = torch.zeros(4, 8, dtype=torch.complex64, device="cuda")
-    with pytest.raises(RuntimeError, match="n2/2 \\+ 1 = 5 input columns"):
-        spectral.irfft2(x, 8)
+        spectral.fft2(_complex(8192, 2), impl=impl)
 
 
 # Every shape with a single-pass kernel (n1, n2 in 4 .. 16, or in 32 .. 256 with the half spectrum
@@ -161,12 +167,12 @@ FUSED_IMPLS = ["stockham_r4", "stockham_r8", "stockham_r8_table"]
 @pytest.mark.parametrize(("n1", "n2"), FUSED_SHAPES)
 def test_single_pass_rfft2_and_irfft2(rng, impl, n1, n2):
     x = random_real(rng, (17, n1, n2))
-    y = spectral.rfft2(cuda(x), impl=impl)
+    y = spectral.rfft2(dev(x), impl=impl)
     assert_transform_close(y, ref.rfft2(x), n1 * n2, axes=AXES)
-    two_pass = spectral.rfft2(cuda(x), impl=impl, columns="transpose")
+    two_pass = spectral.rfft2(dev(x), impl=impl, columns="transpose")
     assert_transform_close(y, two_pass.cpu().numpy(), n1 * n2, axes=AXES)
     spectrum = random_complex(rng, (17, n1, n2 // 2 + 1))
-    back = spectral.irfft2(cuda(spectrum), n2, impl=impl)
+    back = spectral.irfft2(dev(spectrum), n2, impl=impl)
     assert_transform_close(back, ref.irfft2(spectrum, (n1, n2)), n1 * n2, axes=AXES)
 
 
@@ -177,20 +183,20 @@ def test_single_pass_rfft2_and_irfft2(rng, impl, n1, n2):
 # 512-row shapes cover C3's column kernel from one 16-column tile per array (512 x 32) to 256.
 COLUMN_FIRST_SHAPES = [(1, 64), (2, 32), (8, 256), (32, 512), (256, 256), (512, 512), (2048, 64),
                        (16, 4096), (4, 8192), (512, 32), (512, 64), (512, 2048), (512, 8192)]
-STOCKHAM_IMPLS = [impl for impl in spectral.FFT_IMPLS if impl.startswith("stockham")]
+STOCKHAM_IMPLS = STOCKHAM
 
 
 @pytest.mark.parametrize("impl", STOCKHAM_IMPLS)
 @pytest.mark.parametrize(("n1", "n2"), COLUMN_FIRST_SHAPES)
 def test_column_first_rfft2_and_irfft2(rng, impl, n1, n2):
     x = random_real(rng, (3, n1, n2))
-    y = spectral.rfft2(cuda(x), impl=impl)
+    y = spectral.rfft2(dev(x), impl=impl)
     assert_transform_close(y, ref.rfft2(x), n1 * n2, axes=AXES)
     spectrum = random_complex(rng, (3, n1, n2 // 2 + 1))
-    back = spectral.irfft2(cuda(spectrum), n2, impl=impl)
+    back = spectral.irfft2(dev(spectrum), n2, impl=impl)
     assert_transform_close(back, ref.irfft2(spectrum, (n1, n2)), n1 * n2, axes=AXES)
     hermitian = ref.rfft2(x).astype(np.complex64)
-    again = spectral.irfft2(cuda(hermitian), n2, impl=impl)
+    again = spectral.irfft2(dev(hermitian), n2, impl=impl)
     assert_transform_close(again, x, n1 * n2, tol=2 * fft_tolerance(n1 * n2), axes=AXES)
 
 
@@ -204,11 +210,11 @@ FUSED_C2C_SHAPES = [(4, 4), (8, 8), (16, 16), (32, 32), (32, 64), (64, 32), (64,
 @pytest.mark.parametrize(("n1", "n2"), FUSED_C2C_SHAPES)
 def test_single_pass_fft2_and_ifft2(rng, impl, n1, n2):
     x = random_complex(rng, (17, n1, n2))
-    y = spectral.fft2(cuda(x), impl=impl)
+    y = spectral.fft2(dev(x), impl=impl)
     assert_transform_close(y, ref.fft2(x), n1 * n2, axes=AXES)
-    two_pass = spectral.fft2(cuda(x), impl=impl, columns="transpose")
+    two_pass = spectral.fft2(dev(x), impl=impl, columns="transpose")
     assert_transform_close(y, two_pass.cpu().numpy(), n1 * n2, axes=AXES)
-    back = spectral.fft2(cuda(x), inverse=True, impl=impl)
+    back = spectral.fft2(dev(x), inverse=True, impl=impl)
     assert_transform_close(back, ref.ifft2(x), n1 * n2, axes=AXES)
 
 
@@ -221,12 +227,12 @@ LONG_COLUMN_SHAPES = [(2048, 32), (2048, 64), (4096, 32), (4096, 128)]
 @pytest.mark.parametrize(("n1", "n2"), LONG_COLUMN_SHAPES)
 def test_long_columns(rng, impl, n1, n2):
     x = random_complex(rng, (2, n1, n2))
-    assert_transform_close(spectral.fft2(cuda(x), impl=impl), ref.fft2(x), n1 * n2, axes=AXES)
-    assert_transform_close(spectral.fft2(cuda(x), inverse=True, impl=impl), ref.ifft2(x),
+    assert_transform_close(spectral.fft2(dev(x), impl=impl), ref.fft2(x), n1 * n2, axes=AXES)
+    assert_transform_close(spectral.fft2(dev(x), inverse=True, impl=impl), ref.ifft2(x),
                            n1 * n2, axes=AXES)
     r = random_real(rng, (2, n1, 2 * n2))
-    assert_transform_close(spectral.rfft2(cuda(r), impl=impl), ref.rfft2(r), 2 * n1 * n2,
+    assert_transform_close(spectral.rfft2(dev(r), impl=impl), ref.rfft2(r), 2 * n1 * n2,
                            axes=AXES)
     spectrum = random_complex(rng, (2, n1, n2 + 1))
-    assert_transform_close(spectral.irfft2(cuda(spectrum), 2 * n2, impl=impl),
+    assert_transform_close(spectral.irfft2(dev(spectrum), 2 * n2, impl=impl),
                            ref.irfft2(spectrum, (n1, 2 * n2)), 2 * n1 * n2, axes=AXES)

@@ -1,11 +1,17 @@
-"""The CPU oracle, checked before any kernel is compared against it: the float64 references
-against the DFT's definition, closed forms and each other; the tolerance policy against float32
-rounding and production FFTs (reference tests/test_reference.py)."""
+"""The CPU oracle, checked before any kernel is compared against it (reference
+tests/test_reference.py covers the same ground): the float64 references against the DFT written
+out as sums, closed forms, invariants (Parseval, conjugation, Hermitian symmetry) and the golden
+mode-index fixture; mistakes planted in copies of them must fail those checks. Then the
+tolerance policy against float32 FFTs and the values it is quoted with."""
+
+import json
+from pathlib import Path
 
 import numpy as np
 import pytest
 import torch
 
+from mode_labels import LAYOUT_CASES, hermitian_join, labelled_half_spectrum, rounded
 from oracle import reference as ref
 from oracle.tolerance import (
     FLOAT32_EPS,
@@ -16,13 +22,58 @@ from oracle.tolerance import (
     random_real,
 )
 
-# --- the references ------------------------------------------------------------------------
+GOLDEN = Path(__file__).parent / "golden"
 
 
-@pytest.mark.parametrize("n", [1, 2, 3, 5, 8, 12, 16, 31, 64])
-def test_fft_matches_the_definition(rng, n):
+def dft_by_sums(x: np.ndarray) -> np.ndarray:
+    """X[k] = sum_m x[m] (cos - i sin)(2 pi k m / n), the angle reduced exactly in integers."""
+    n = x.shape[-1]
+    km = np.outer(np.arange(n), np.arange(n)) % n
+    angle = 2 * np.pi * km / n
+    return x.astype(np.complex128) @ (np.cos(angle) - 1j * np.sin(angle)).T
+
+
+# --- the 1D references -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 8, 12, 16, 31, 64, 100])
+def test_fft_is_the_dft_sum(rng, n):
     x = random_complex(rng, (4, n))
-    np.testing.assert_allclose(ref.fft(x), ref.dft(x), rtol=0, atol=1e-10 * n)
+    got = ref.fft(x)
+    assert np.max(np.abs(got - dft_by_sums(x))) <= 1e-10 * n
+    assert np.max(np.abs(ref.dft(x) - dft_by_sums(x))) <= 1e-10 * n  # the oracle's own sum
+
+
+@pytest.mark.parametrize("n", [2, 64, 4096])
+def test_fft_keeps_energy_and_ifft_is_its_conjugate_form(rng, n):
+    x = random_complex(rng, (3, n)).astype(np.complex128)
+    spectrum = ref.fft(x)
+    # Parseval: sum |x|^2 = sum |X|^2 / n.
+    np.testing.assert_allclose(np.sum(np.abs(spectrum) ** 2, -1) / n, np.sum(np.abs(x) ** 2, -1),
+                               rtol=1e-12)
+    # ifft(X) = conj(fft(conj X)) / n, and it returns x.
+    np.testing.assert_allclose(ref.ifft(spectrum), np.conj(ref.fft(np.conj(spectrum))) / n,
+                               rtol=0, atol=1e-13)
+    assert np.max(np.abs(ref.ifft(spectrum) - x)) <= 1e-12
+
+
+@pytest.mark.parametrize("n", [8, 9, 64])
+def test_rfft_is_the_cosine_and_sine_sums_for_k_up_to_n_over_2(rng, n):
+    x = random_real(rng, (3, n)).astype(np.float64)
+    k = np.arange(n // 2 + 1)[:, None]
+    m = np.arange(n)[None, :]
+    angle = 2 * np.pi * (k * m % n) / n
+    expected = x @ np.cos(angle).T - 1j * (x @ np.sin(angle).T)
+    assert np.max(np.abs(ref.rfft(x) - expected)) <= 1e-11 * n
+
+
+@pytest.mark.parametrize("n", [8, 9, 64])
+def test_irfft_rebuilds_the_real_signal_from_its_half_spectrum(rng, n):
+    x = random_real(rng, (3, n)).astype(np.float64)
+    half = ref.rfft(x)
+    assert np.max(np.abs(ref.irfft(half, n) - x)) <= 1e-12
+    # and the full spectrum it stands for is Hermitian: X[n - k] = conj X[k]
+    full = ref.fft(x)
+    np.testing.assert_allclose(full[..., 1:][..., ::-1], np.conj(full[..., 1:]), atol=1e-11)
 
 
 def test_dft_of_closed_forms():
@@ -39,24 +90,6 @@ def test_dft_of_closed_forms():
     np.testing.assert_allclose(ref.fft(tone), want, atol=1e-11)
 
 
-@pytest.mark.parametrize("n", [2, 64, 4096])
-def test_ifft_inverts_fft(rng, n):
-    x = random_complex(rng, (3, n))
-    np.testing.assert_allclose(ref.ifft(ref.fft(x)), x, rtol=0, atol=1e-12)
-
-
-@pytest.mark.parametrize("n", [8, 9, 64])
-def test_rfft_is_the_nonnegative_half_of_fft(rng, n):
-    x = random_real(rng, (3, n))
-    np.testing.assert_allclose(ref.rfft(x), ref.fft(x)[..., : n // 2 + 1], rtol=0, atol=1e-10)
-
-
-@pytest.mark.parametrize("n", [8, 9, 64])
-def test_irfft_inverts_rfft(rng, n):
-    x = random_real(rng, (3, n))
-    np.testing.assert_allclose(ref.irfft(ref.rfft(x), n), x, rtol=0, atol=1e-12)
-
-
 def test_irfft_ignores_imaginary_dc_and_nyquist(rng):
     x = random_complex(rng, (2, 9)).astype(np.complex128)
     y = x.copy()
@@ -69,10 +102,16 @@ def test_irfft_ignores_imaginary_dc_and_nyquist(rng):
                                atol=1e-12)
 
 
-def test_fft2_is_row_transforms_then_column_transforms(rng):
-    x = random_complex(rng, (2, 8, 16))
-    rows_then_columns = np.fft.fft(ref.fft(x), axis=-2)
-    np.testing.assert_allclose(ref.fft2(x), rows_then_columns, rtol=0, atol=1e-10)
+@pytest.mark.parametrize(("n1", "n2"), [(2, 8), (8, 16), (5, 3)])
+def test_fft2_is_the_2d_dft_sum_and_separates_in_either_order(rng, n1, n2):
+    x = random_complex(rng, (2, n1, n2))
+    a, b = np.arange(n1), np.arange(n2)
+    kernel = np.exp(-2j * np.pi * ((np.multiply.outer(a, a) % n1)[:, None, :, None] / n1
+                                   + (np.multiply.outer(b, b) % n2)[None, :, None, :] / n2))
+    by_sum = np.einsum("zmn,pqmn->zpq", x.astype(np.complex128), kernel)
+    np.testing.assert_allclose(ref.fft2(x), by_sum, rtol=0, atol=1e-10 * n1 * n2)
+    columns_first = ref.fft(np.fft.fft(x.astype(np.complex128), axis=-2))
+    np.testing.assert_allclose(ref.fft2(x), columns_first, rtol=0, atol=1e-10 * n1 * n2)
 
 
 def idft_by_sum(modes: np.ndarray, n: int, freqs) -> np.ndarray:
@@ -175,14 +214,35 @@ def test_the_pruned_pins_reject_plausible_mistakes(rng):
         assert not np.allclose(bad, defn, rtol=0, atol=1e-6)
 
 
-def test_rfft2_truncate_keeps_the_lowest_modes(rng):
-    # The reference's known answer (test_reference.py:53-59), restated.
-    x = random_real(rng, (2, 16, 16))
-    full = ref.rfft2(x)
-    modes = ref.rfft2_truncate(x, m1=3, m2=4)
-    assert modes.shape == (2, 6, 4)
-    np.testing.assert_array_equal(modes[..., :3, :], full[..., :3, :4])
-    np.testing.assert_array_equal(modes[..., 3:, :], full[..., 13:, :4])
+def test_rfft2_truncate_takes_the_golden_positions_of_the_half_spectrum(rng):
+    # tests/golden/modes_index.json holds, per shape, the half-spectrum position of every mode
+    # slot, enumerated from the frequency semantics alone. The oracle's modes must be exactly the
+    # values at those positions (the reference's known answer, test_reference.py:53-59, is the
+    # (16, 16, 3, 4) case).
+    for case in json.loads((GOLDEN / "modes_index.json").read_text()):
+        n1, n2, m1, m2 = case["n1"], case["n2"], case["m1"], case["m2"]
+        x = random_real(rng, (2, n1, n2))
+        flat = ref.rfft2(x).reshape(2, -1)
+        modes = ref.rfft2_truncate(x, m1, m2)
+        assert modes.shape == (2, 2 * m1, m2)
+        np.testing.assert_array_equal(modes.reshape(2, -1), flat[:, case["positions"]])
+
+
+def test_labelled_spectra_of_the_layout_tests_are_exact_targets():
+    # The GPU layout test (test_pruned.py) labels the kept modes with Gaussian integers and
+    # compares rounded results: the labels must be distinct, survive a float64 round trip
+    # through a real field, and be a fixed point of the real inverse's Hermitian join.
+    for n1, n2, m1, m2 in LAYOUT_CASES:
+        full, kept = labelled_half_spectrum(n1, n2, m1, m2)
+        assert np.count_nonzero(kept) == kept.size
+        assert len(set(kept[0].tolist())) == kept.shape[1]
+        assert np.array_equal(rounded(ref.rfft2(ref.irfft2(full, (n1, n2)))), full)
+        assert np.array_equal(hermitian_join(full, n2), full)
+    # A mistake planted in the join (rows mirrored without the wrap of row 0) is caught.
+    full, _ = labelled_half_spectrum(16, 16, 3, 4)
+    shifted = full.copy()
+    shifted[..., :, 0] = (full[..., :, 0] + np.conj(full[..., ::-1, 0])) / 2
+    assert not np.array_equal(shifted, hermitian_join(full, 16))
 
 
 def test_truncation_layout_by_frequency(rng):
@@ -199,18 +259,26 @@ def test_truncation_layout_by_frequency(rng):
             assert abs(modes[r, c] - want) < 1e-10
 
 
-def test_keeping_every_mode_round_trips(rng):
-    x = random_real(rng, (2, 8, 8))
-    modes = ref.rfft2_truncate(x, m1=4, m2=5)
-    np.testing.assert_allclose(ref.irfft2_from_modes(modes, (8, 8)), x, rtol=0, atol=1e-12)
+@pytest.mark.parametrize(("n1", "n2"), [(8, 8), (4, 16), (16, 2)])
+def test_keeping_the_whole_half_spectrum_loses_nothing(rng, n1, n2):
+    # m1 = n1/2 rows of each sign and m2 = n2/2 + 1 columns are every stored frequency.
+    x = random_real(rng, (2, n1, n2))
+    modes = ref.rfft2_truncate(x, n1 // 2, n2 // 2 + 1)
+    assert np.max(np.abs(ref.irfft2_from_modes(modes, (n1, n2)) - x)) <= 1e-12
 
 
-def test_truncation_is_a_low_pass_filter():
+@pytest.mark.parametrize(("kept", "dropped"), [([(1, 2), (-3, 1)], [(10, 12), (-7, 9)]),
+                                               ([(0, 3), (2, 0)], [(4, 1), (-12, 5)])])
+def test_truncation_passes_kept_cosines_and_removes_the_rest(kept, dropped):
+    # Cosines at frequencies (f1, f2) inside m1 = m2 = 4 come back unchanged; those outside go.
     i, j = np.meshgrid(np.arange(32), np.arange(32), indexing="ij")
-    low = np.cos(2 * np.pi * (1 * i + 2 * j) / 32)
-    high = np.cos(2 * np.pi * (10 * i + 12 * j) / 32)
-    modes = ref.rfft2_truncate(low + high, m1=4, m2=4)
-    np.testing.assert_allclose(ref.irfft2_from_modes(modes, (32, 32)), low, rtol=0, atol=1e-12)
+
+    def cosines(freqs):
+        return sum(np.cos(2 * np.pi * (f1 * i + f2 * j) / 32) for f1, f2 in freqs)
+
+    modes = ref.rfft2_truncate(cosines(kept) + cosines(dropped), m1=4, m2=4)
+    back = ref.irfft2_from_modes(modes, (32, 32))
+    assert np.max(np.abs(back - cosines(kept))) <= 1e-12
 
 
 def test_reference_rejects_bad_modes():
@@ -226,27 +294,32 @@ def test_reference_rejects_bad_modes():
 
 
 @pytest.mark.parametrize("n", POW2_SIZES)
-def test_policy_accepts_float32_rounding_of_the_exact_result(rng, n):
+def test_policy_passes_numpys_own_single_precision_fft(rng, n):
+    # pocketfft computes complex64 in single precision: a production float32 FFT must pass.
     x = random_complex(rng, (8, n))
-    exact = ref.fft(x)
-    assert_transform_close(exact.astype(np.complex64), exact, n)
+    single = np.fft.fft(x.astype(np.complex64), axis=-1)
+    assert single.dtype == np.complex64
+    assert_transform_close(single, ref.fft(x), n)
 
 
-def test_policy_rejects_one_bad_transform_in_a_batch(rng):
-    n = 1024
-    x = random_complex(rng, (64, n))
-    exact = ref.fft(x)
-    actual = exact.copy()
-    actual[17, 5] += 10 * fft_tolerance(n) * np.linalg.norm(exact[17])
-    with pytest.raises(AssertionError, match=r"exceeds the tolerance .* in transform \(17,\)"):
-        assert_transform_close(actual, exact, n)
+def test_policy_names_the_transform_that_fails():
+    n = 256
+    exact = ref.fft(random_complex(np.random.default_rng(7), (4, 8, n)))
+    bad = exact.copy()
+    bad[2, 5, 100] += 20 * fft_tolerance(n) * np.linalg.norm(exact[2, 5])
+    with pytest.raises(AssertionError, match=r"exceeds the tolerance .* in transform \(2, 5\)"):
+        assert_transform_close(bad, exact, n)
+    bad[2, 5, 100] = exact[2, 5, 100] + 0.5 * fft_tolerance(n) * np.linalg.norm(exact[2, 5])
+    assert_transform_close(bad, exact, n)  # half the allowance passes
 
 
-def test_policy_limit_is_eight_eps_per_stage():
-    assert fft_tolerance(4096) == pytest.approx(8 * FLOAT32_EPS * 12)
-    assert fft_tolerance(1024) == pytest.approx(9.5367e-06, rel=1e-4)
-    assert fft_tolerance(2) == pytest.approx(8 * FLOAT32_EPS)
-    assert fft_tolerance(1) == pytest.approx(8 * FLOAT32_EPS)  # max(1, log2 N)
+@pytest.mark.parametrize(("n", "quoted"), [(1, 9.54e-7), (2, 9.54e-7), (1024, 9.54e-6),
+                                          (4096, 1.14e-5), (128 * 128, 1.34e-5),
+                                          (512 * 512, 1.72e-5)])
+def test_policy_values_are_eight_float32_epsilons_per_stage(n, quoted):
+    assert FLOAT32_EPS == 2.0 ** -23
+    assert fft_tolerance(n) == pytest.approx(quoted, rel=5e-3)  # quoted to 3 digits
+    assert fft_tolerance(n) == 8 * 2.0 ** -23 * max(1, int(np.log2(n)))
 
 
 def test_policy_catches_plausible_mistakes(rng):
@@ -262,14 +335,13 @@ def test_policy_catches_plausible_mistakes(rng):
             assert_transform_close(bad, good, n)
 
 
-def test_torch_fft_meets_the_policy_on_cpu(rng):
-    for n in POW2_SIZES:
-        x = random_complex(rng, (64, n))
-        assert_transform_close(torch.fft.fft(torch.from_numpy(x)), ref.fft(x), n)
-
-
-def test_torch_rfft2_meets_the_policy_on_cpu(rng):
-    for n1, n2 in [(64, 64), (128, 256)]:
-        x = random_real(rng, (8, n1, n2))
-        actual = torch.fft.rfft2(torch.from_numpy(x))
-        assert_transform_close(actual, ref.rfft2(x), n1 * n2, axes=(-2, -1))
+@pytest.mark.parametrize("shape", [(64, 2), (64, 1024), (16, 4096), (8, 64, 64), (4, 128, 256)])
+def test_torch_fft_on_the_cpu_meets_the_policy(rng, shape):
+    if len(shape) == 2:
+        x = random_complex(rng, shape)
+        assert_transform_close(torch.fft.fft(torch.from_numpy(x)), ref.fft(x), shape[-1])
+    else:
+        x = random_real(rng, shape)
+        n = shape[-2] * shape[-1]
+        assert_transform_close(torch.fft.rfft2(torch.from_numpy(x)), ref.rfft2(x), n,
+                               axes=(-2, -1))
