@@ -12,8 +12,13 @@
 //                     half-spectrum rows in the column pass
 //   RowsThenColumns   row kernel, then the strided column kernel in place (or, for the
 //                     inverse real transform, columns out of place then the real rows)
-//   Transposes        the "transpose" method, every implementation: rows, a transpose, the
-//                     columns as contiguous rows, a transpose back (remap.hip's tiled kernel)
+//   TransposedPasses  the "transpose" method for the Stockham implementations: rows stored
+//                     transposed, then the columns as rows of the workspace, stored transposed
+//                     back; the transposes ride on the passes' LDS tiles (fft2_transposed.hpp),
+//                     two HBM round trips instead of the reference's four (fft2d.cu:138-187)
+//   Transposes        the "transpose" method otherwise (naive, and arrays with a side of 1, or
+//                     real rows of 2): rows, a transpose, the columns as contiguous rows, a
+//                     transpose back (remap.hip's tiled kernel)
 //
 // The inverse's 1 / (n1 n2) comes from the 1D passes: 1/n2 in the rows, 1/n1 in the columns.
 
@@ -26,7 +31,7 @@ namespace spx {
 namespace {
 
 enum class Kind { C2c, R2c, C2r };
-enum class Route { SinglePass, ColumnFirst, RowsThenColumns, Transposes };
+enum class Route { SinglePass, ColumnFirst, RowsThenColumns, TransposedPasses, Transposes };
 
 struct Plan2d {
     Route route;
@@ -84,13 +89,19 @@ Plan2d plan_2d(const FftImpl& impl, Columns columns, Kind kind, int n1, int n2, 
     const int w = kind == Kind::C2c ? n2 : n2 / 2 + 1;
     const std::size_t real_rows =
         kind != Kind::C2c && impl.real_needs_work ? values(n1, n2 / 2, batch) : 0;
+    const Fused2dFns* f = impl.fused;
     if (columns == Columns::Transpose) {
+        if (f != nullptr && n1 >= 2 && n2 >= (kind == Kind::C2c ? 2 : 4)) {
+            p.route = Route::TransposedPasses;
+            p.regions = 1;
+            p.region = values(n1, w, batch);
+            return p;
+        }
         p.regions = 2;
         p.region = values(n1, w, batch);
         p.real = real_rows;
         return p;
     }
-    const Fused2dFns* f = impl.fused;
     if (kind == Kind::C2c) {
         p.route = f != nullptr && f->c2c_supports(n1, n2) ? Route::SinglePass
                                                           : Route::RowsThenColumns;
@@ -163,6 +174,9 @@ void fft2_c2c(const FftImpl& impl, Columns columns, const cf32* x, cf32* y, int 
         }
         impl.columns(y, y, n1, n2, batch, direction, stream);
         return;
+    case Route::TransposedPasses:
+        impl.fused->c2c_transposed(x, y, p.at(work, 0), n1, n2, batch, direction, stream);
+        return;
     default: {
         cf32* a = p.at(work, 0);
         cf32* b = p.at(work, 1);
@@ -193,6 +207,9 @@ void fft2_r2c(const FftImpl& impl, Columns columns, const float* x, cf32* y, int
         impl.r2c(x, y, n2, batch * n1, p.real_scratch(work), stream);
         impl.columns(y, y, n1, w, batch, Direction::Forward, stream);
         return;
+    case Route::TransposedPasses:
+        impl.fused->r2c_transposed(x, y, p.at(work, 0), n1, n2, batch, stream);
+        return;
     default: {
         cf32* a = p.at(work, 0);
         cf32* b = p.at(work, 1);
@@ -222,6 +239,9 @@ void fft2_c2r(const FftImpl& impl, Columns columns, const cf32* x, float* y, int
     case Route::RowsThenColumns:
         impl.columns(x, p.at(work, 0), n1, w, batch, Direction::Inverse, stream);
         impl.c2r(p.at(work, 0), y, n2, batch * n1, p.real_scratch(work), stream);
+        return;
+    case Route::TransposedPasses:
+        impl.fused->c2r_transposed(x, y, p.at(work, 0), n1, n2, batch, stream);
         return;
     default: {
         cf32* a = p.at(work, 0);

@@ -74,6 +74,15 @@ struct Fused2dFns {
     // pass then transforms in place (plain stores).
     void (*c2c_rows)(const cf32* x, cf32* y, int n, int batch, Direction direction,
                      hipStream_t stream);
+    // The "transpose" column method in two passes that transpose through their LDS tiles
+    // (fft2_transposed.hpp), n1 >= 2 and n2 >= 2 (complex) or 4 (real): work holds batch arrays
+    // of n2 x n1 (complex) or (n2/2 + 1) x n1 (real) values.
+    void (*c2c_transposed)(const cf32* x, cf32* y, cf32* work, int n1, int n2, int batch,
+                           Direction direction, hipStream_t stream);
+    void (*r2c_transposed)(const float* x, cf32* y, cf32* work, int n1, int n2, int batch,
+                           hipStream_t stream);
+    void (*c2r_transposed)(const cf32* x, float* y, cf32* work, int n1, int n2, int batch,
+                           hipStream_t stream);
 };
 
 // The radio callers (rf.hpp): windowed spectrum of back-to-back frames, and overlap-save FIR.

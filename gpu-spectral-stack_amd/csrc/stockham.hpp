@@ -937,6 +937,69 @@ struct C2cIo {
     }
 };
 
+// The real transforms' pair passes over a group's rows in LDS (row u at lds + u * kStride, value
+// k at pad(k)), one pair (k, m - k) per step, both slots read and written by the same lane, so no
+// lane touches another lane's slots (k = 0 pairs slot 0 with slot m).
+//
+// combine_pairs (forward): the m-point transform Z of the row read as complex becomes the half
+// spectrum X[0 .. m]: E = (Z[k] + conj Z[m-k]) / 2, O = (Z[k] - conj Z[m-k]) / 2i (indices mod m),
+// X[k] = E + exp(-pi i k / m) O, X[m-k] = conj(E - exp(-pi i k / m) O); X[m] lands in slot m.
+template <class P, class G>
+__device__ __forceinline__ void combine_pairs(cf32* lds, int count, int tid)
+{
+    constexpr int m = P::N;
+    using S = Staged<G, m / 2 + 1>;
+    S::each(count, tid, [&](int, int u, int k, bool valid) {
+        if (!valid) {
+            return;
+        }
+        cf32* s = lds + u * P::kStride;
+        const cf32 zk = s[pad(k & (m - 1))];
+        const cf32 zm = s[pad((m - k) & (m - 1))];
+        const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
+        const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
+        const cf32 wo = cmul(twiddle_of<2 * m, false>(k), od);  // exp(-pi i k / m) O
+        s[pad(k)] = cadd(ev, wo);
+        if (k < m - k) {
+            s[pad(m - k)] = cconj(csub(ev, wo));
+        }
+    });
+}
+
+// prepare_pairs (inverse): the half spectrum X[0 .. m] becomes the m-point inverse's input Z:
+// E = (X[k] + conj X[m-k]) / 2, O = exp(pi i k / m) (X[k] - conj X[m-k]) / 2, Z[k] = E + i O,
+// Z[m-k] = conj(E - i O), the imaginary parts of X[0] and X[m] dropped; `scale` rides on the
+// halves.
+template <class P, class G>
+__device__ __forceinline__ void prepare_pairs(cf32* lds, int count, int tid, float scale)
+{
+    constexpr int m = P::N;
+    const float half = 0.5f * scale;
+    using S = Staged<G, m / 2 + 1>;
+    S::each(count, tid, [&](int, int u, int k, bool valid) {
+        if (!valid) {
+            return;
+        }
+        cf32* s = lds + u * P::kStride;
+        cf32 xk = s[pad(k)];
+        cf32 xm = s[pad(m - k)];
+        if (k == 0) {
+            xk.im = 0.0f;
+            xm.im = 0.0f;
+        }
+        const cf32 ev{half * (xk.re + xm.re), half * (xk.im - xm.im)};
+        const cf32 d{half * (xk.re - xm.re), half * (xk.im + xm.im)};
+        const cf32 od = cmul(d, twiddle_of<2 * m, true>(k));  // d exp(pi i k / m)
+        const cf32 iod{-od.im, od.re};
+        if (k < m) {
+            s[pad(k)] = cadd(ev, iod);
+        }
+        if (k > 0 && k < m - k) {
+            s[pad(m - k)] = cconj(csub(ev, iod));
+        }
+    });
+}
+
 // Real input (forward). A row of n = 2m reals is read as m complex values z[j] = x[2j] + i x[2j+1]
 // (the same bytes), an m-point forward transform gives Z, and the store combines pairs:
 //   E = (Z[k] + conj Z[m-k]) / 2,  O = (Z[k] - conj Z[m-k]) / 2i,  w = exp(-pi i k / m),
@@ -1067,25 +1130,7 @@ struct R2cIoT {
             return;  // stored by final
         }
         if constexpr (!direct_combine<P>()) {
-            // 1. Combine in place: pair k reads Z[k] and Z[m-k] and writes X[k] and X[m-k] to the
-            //    same two slots (k = 0 reads slot 0 and writes X[0] there and X[m] into slot m),
-            //    so no lane touches another lane's slots.
-            using S = Staged<G, m / 2 + 1>;
-            S::each(count, tid, [&](int, int u, int k, bool valid) {
-                if (!valid) {
-                    return;
-                }
-                cf32* s = lds + u * P::kStride;
-                const cf32 zk = s[pad(k & (m - 1))];
-                const cf32 zm = s[pad((m - k) & (m - 1))];
-                const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
-                const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
-                const cf32 wo = cmul(twiddle_of<2 * m, false>(k), od);  // exp(-pi i k / m) O
-                s[pad(k)] = cadd(ev, wo);
-                if (k < m - k) {
-                    s[pad(m - k)] = cconj(csub(ev, wo));
-                }
-            });
+            combine_pairs<P, G>(lds, count, tid);
             lds_sync<G::kWave>();
         }
         // 2. The first `keep` values of each row, stored contiguously.
@@ -1170,31 +1215,7 @@ struct C2rIo {
         });
         if constexpr (!direct_prepare<P>()) {
             lds_sync<G::kWave>();
-            // Prepare Z in place, one pair (k, m-k) per step: both read and written by one lane.
-            const float half = 0.5f * scale;
-            using S = Staged<G, m / 2 + 1>;
-            S::each(count, tid, [&](int, int u, int k, bool valid) {
-                if (!valid) {
-                    return;
-                }
-                cf32* s = lds + u * P::kStride;
-                cf32 xk = s[pad(k)];
-                cf32 xm = s[pad(m - k)];
-                if (k == 0) {
-                    xk.im = 0.0f;
-                    xm.im = 0.0f;
-                }
-                const cf32 ev{half * (xk.re + xm.re), half * (xk.im - xm.im)};
-                const cf32 d{half * (xk.re - xm.re), half * (xk.im + xm.im)};
-                const cf32 od = cmul(d, twiddle_of<2 * m, true>(k));  // d exp(pi i k / m)
-                const cf32 iod{-od.im, od.re};
-                if (k < m) {
-                    s[pad(k)] = cadd(ev, iod);
-                }
-                if (k > 0 && k < m - k) {
-                    s[pad(m - k)] = cconj(csub(ev, iod));
-                }
-            });
+            prepare_pairs<P, G>(lds, count, tid, scale);
         }
     }
 

@@ -10,6 +10,7 @@
 #include "fft2_fused.hpp"
 #include "fft2_modes.hpp"
 #include "fft2_pairs.hpp"
+#include "fft2_transposed.hpp"
 #include "fft_api.hpp"
 #include "rf.hpp"
 #include "stockham.hpp"
@@ -1194,10 +1195,68 @@ struct Fused2dDriver {
               2LL * batch * rows.pairs, stream);
     }
 
+    // The transpose column method in two passes (fft2_transposed.hpp), on the column plans
+    // (T = 16 transforms per workgroup up to N = 512: 128-byte runs on the transposed side).
+    // work: batch arrays of n2 x n1 (complex) or (n2/2 + 1) x n1 (real) values.
+    template <class Io>
+    static void columns_plan(int n, bool inverse, const Io& io, long long transforms,
+                             hipStream_t stream)
+    {
+        if (inverse) {
+            dev::dispatch_columns<R, true, Table>(n, io, transforms, stream);
+        } else {
+            dev::dispatch_columns<R, false, Table>(n, io, transforms, stream);
+        }
+    }
+
+    // Rows of n2 (x -> work, stored transposed), then the columns as rows of n1 (work -> y,
+    // stored transposed back). The inverse's 1/n2 and 1/n1 ride on the two passes' stores.
+    static void c2c_transposed(const cf32* x, cf32* y, cf32* work, int n1, int n2, int batch,
+                               Direction direction, hipStream_t stream)
+    {
+        const bool inverse = direction == Direction::Inverse;
+        const float s2 = inverse ? 1.0f / static_cast<float>(n2) : 1.0f;
+        const float s1 = inverse ? 1.0f / static_cast<float>(n1) : 1.0f;
+        columns_plan(n2, inverse, dev::RowsToTransposedIo{x, work, n1, s2, true, false},
+                     static_cast<long long>(batch) * n1, stream);
+        columns_plan(n1, inverse, dev::RowsToTransposedIo{work, y, n2, s1, false, true},
+                     static_cast<long long>(batch) * n2, stream);
+    }
+
+    // Real rows of n2 = 2m to half spectra, stored transposed (x -> work); then the m + 1
+    // columns as rows of n1 (work -> y, stored transposed back).
+    static void r2c_transposed(const float* x, cf32* y, cf32* work, int n1, int n2, int batch,
+                               hipStream_t stream)
+    {
+        const int m = n2 / 2;
+        columns_plan(m, false,
+                     dev::R2cRowsToTransposedIo{reinterpret_cast<const cf32*>(x), work, n1},
+                     static_cast<long long>(batch) * n1, stream);
+        columns_plan(n1, false, dev::RowsToTransposedIoT<8>{work, y, m + 1, 1.0f, false, false},
+                     static_cast<long long>(batch) * (m + 1), stream);
+    }
+
+    // The m + 1 columns of the half spectra read transposed, inverted and written as rows of n1
+    // (x -> work); then the real rows read transposed from there (work -> y).
+    static void c2r_transposed(const cf32* x, float* y, cf32* work, int n1, int n2, int batch,
+                               hipStream_t stream)
+    {
+        const int m = n2 / 2;
+        columns_plan(n1, true,
+                     dev::TransposedToRowsIoT<8>{x, work, m + 1, 1.0f / static_cast<float>(n1),
+                                                 false, false},
+                     static_cast<long long>(batch) * (m + 1), stream);
+        columns_plan(m, true,
+                     dev::C2rTransposedToRowsIo{work, reinterpret_cast<cf32*>(y), n1,
+                                                1.0f / static_cast<float>(m)},
+                     static_cast<long long>(batch) * n1, stream);
+    }
+
     static Fused2dFns fns()
     {
-        return {&supports, &r2c,          &c2r, &r2c_columns, &r2c_rows,
-                &c2r_rows, &c2c_supports, &c2c, &c2c_rows};
+        return {&supports,       &r2c,           &c2r,           &r2c_columns, &r2c_rows,
+                &c2r_rows,       &c2c_supports,  &c2c,           &c2c_rows,    &c2c_transposed,
+                &r2c_transposed, &c2r_transposed};
     }
 
     static void c2r(const cf32* x, float* y, int n1, int n2, int m1, int w, int batch,
