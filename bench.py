@@ -49,7 +49,16 @@ BATCH = 16384
 POINTS = N * BATCH
 BYTES_PER_DIRECTION = 16 * POINTS  # 268,435,456
 PEAK_GBPS = 8000.0
-SETS = 4  # 4 x (x, y, z) x 128 MiB = 1.5 GiB in rotation
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def rotation(input_bytes: int) -> int:
+    """Buffer sets so that the inputs in rotation total at least twice the Infinity Cache: a
+    launch then reads data that the launches since its set's last use have evicted."""
+    return max(2, -(-2 * MALL_BYTES // int(input_bytes)))
+
+
+SETS = rotation(BYTES_PER_DIRECTION // 2)  # 4 x (x, y, z) x 128 MiB = 1.5 GiB in rotation
 
 
 # Secondary row groups, in the order they run: C-ABI timings of the 2D and pruned configurations,
@@ -317,9 +326,10 @@ def secondary_rows(impl: str, dev, later: list) -> dict:
     """The other configurations of the metric, each next to rocFFT (through torch.fft) on the same
     shape: C2 real transforms at n = 1024, C3 rfft2 / irfft2 at 128^2 x 1024 and 512^2 x 64 (both
     column methods: strided, the default, and transpose), C4 pruned transforms on
-    [64, 32, 128, 128] with m1 = m2 = 16, and rocFFT on the C1 shape. Inputs rotate over three
-    sets so no call reads what the previous one left in the cache. rocFFT's rows are timed by what
-    this appends to `later`, after every row of this stack."""
+    [64, 32, 128, 128] with m1 = m2 = 16, and rocFFT on the C1 shape. Inputs rotate over enough
+    sets to total twice the Infinity Cache (rotation()), so no call reads what an earlier one
+    left there. rocFFT's rows are timed by what this appends to `later`, after every row of this
+    stack."""
     import torch
 
     import spectral
@@ -339,8 +349,11 @@ def secondary_rows(impl: str, dev, later: list) -> dict:
     ours = []    # (row name, bytes, fn, inputs, rocFFT row)
     theirs = {}  # rocFFT row -> (fn, inputs)
 
+    def sets(make, one_bytes):
+        return [make() for _ in range(rotation(one_bytes))]
+
     # C2: real transforms, n = 1024, 16384 rows.
-    xr = [torch.randn(16384, 1024, device=dev, generator=g) for _ in range(3)]
+    xr = sets(lambda: torch.randn(16384, 1024, device=dev, generator=g), 64 << 20)
     xh = [torch.fft.rfft(x) for x in xr]
     work = fft_real_work(1024, 16384)[1]
     ours.append(("c2_r2c_1024", work, lambda x: spectral.rfft(x, impl=impl), xr, "r2c"))
@@ -349,7 +362,7 @@ def secondary_rows(impl: str, dev, later: list) -> dict:
     theirs["c2r"] = (lambda x: torch.fft.irfft(x, 1024), xh)
     # C3: 2D real transforms, both column methods.
     for n, arrays in ((128, 1024), (512, 64)):
-        xs = [torch.randn(arrays, n, n, device=dev, generator=g) for _ in range(3)]
+        xs = sets(lambda: torch.randn(arrays, n, n, device=dev, generator=g), 64 << 20)
         hs = [torch.fft.rfft2(x) for x in xs]
         work = fft2_real_work(n, n, arrays)[1]
         ours.append((f"c3_rfft2_{n}", work, lambda x: spectral.rfft2(x, impl=impl), xs,
@@ -365,8 +378,10 @@ def secondary_rows(impl: str, dev, later: list) -> dict:
         theirs[f"rfft2_{n}"] = (torch.fft.rfft2, xs)
         theirs[f"irfft2_{n}"] = (lambda x, n=n: torch.fft.irfft2(x, s=(n, n)), hs)
     # C4: FNO pruned transforms, [64, 32, 128, 128] <-> modes [64, 32, 32, 16].
-    xp = [torch.randn(64, 32, 128, 128, device=dev, generator=g) for _ in range(3)]
-    mp = [spectral.rfft2_truncated(x, 16, 16, impl=impl) for x in xp]
+    xp = sets(lambda: torch.randn(64, 32, 128, 128, device=dev, generator=g), 128 << 20)
+    # The inverse's input is 8 MiB of modes: 64 sets of them.
+    mp = sets(lambda: torch.randn(64, 32, 32, 16, dtype=torch.complex64, device=dev,
+                                  generator=g), 8 << 20)
     work = fft2_modes_work(128, 128, 16, 16, 2048)[1]
 
     def rocfft_gather(x):
@@ -386,7 +401,8 @@ def secondary_rows(impl: str, dev, later: list) -> dict:
     theirs["modes_f"] = (rocfft_gather, xp)
     theirs["modes_i"] = (rocfft_scatter, mp)
     # rocFFT (through torch.fft) on the C1 shape, forward.
-    xc = [torch.randn(BATCH, N, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
+    xc = sets(lambda: torch.randn(BATCH, N, dtype=torch.complex64, device=dev, generator=g),
+              128 << 20)
     theirs["c1"] = (torch.fft.fft, xc)
     torch.cuda.synchronize()
 
@@ -409,8 +425,8 @@ def secondary_rows(impl: str, dev, later: list) -> dict:
 def sweep_rows(lib, impl: int, dev, stream, later: list) -> dict:
     """BASELINE C2's sweep and C1's sizes: C2C, R2C and C2R at n = 2, 4, ..., 4096 with
     batch = 2^24 / n, through the C ABI on `stream`, next to rocFFT (torch.fft) on the same shapes.
-    Three buffer sets of 2^24 complex values each (384 MiB per side, 768 MiB in rotation) serve
-    every size. The sizes are interleaved: each of 9 rounds times 20 launches of every (op, n),
+    Eight buffer sets of 2^24 complex values each (1 GiB per side) serve every size: the real
+    transforms' 64 MiB inputs then total 512 MiB in rotation, twice the Infinity Cache. The sizes are interleaved: each of 9 rounds times 20 launches of every (op, n),
     after 2 untimed ones, so a transient slowdown of the device lands in a round or two of each
     row instead of all of one row's; a row reports the median round. rocFFT's columns are added
     by what this appends to `later`. Rows are
@@ -425,8 +441,10 @@ def sweep_rows(lib, impl: int, dev, stream, later: list) -> dict:
     sptr = ctypes.c_void_p(stream.cuda_stream)
     g = torch.Generator(device=dev).manual_seed(2)
     total = 1 << 24
-    ins = [torch.randn(total, dtype=torch.complex64, device=dev, generator=g) for _ in range(3)]
-    outs = [torch.empty(total, dtype=torch.complex64, device=dev) for _ in range(3)]
+    nsets = rotation(4 * total)  # the smallest input: 2^24 float32 values
+    ins = [torch.randn(total, dtype=torch.complex64, device=dev, generator=g)
+           for _ in range(nsets)]
+    outs = [torch.empty(total, dtype=torch.complex64, device=dev) for _ in range(nsets)]
     torch.cuda.synchronize()
     vp = ctypes.c_void_p
 
@@ -470,7 +488,7 @@ def sweep_rows(lib, impl: int, dev, stream, later: list) -> dict:
         b = torch.cuda.Event(enable_timing=True)
         a.record(on)
         for i in range(20):
-            run(i % 3)
+            run(i % nsets)
         b.record(on)
         b.synchronize()
         return a.elapsed_time(b) / 20 * 1e3
@@ -527,16 +545,16 @@ def capi_rows(lib, impl: int, dev, stream) -> dict:
         check(query(*args, ctypes.byref(count)))
         return torch.empty(max(1, count.value), dtype=torch.complex64, device=dev)
 
-    def time_calls(call):
+    def time_calls(call, k):
         for i in range(3):
-            call(i % 3)
+            call(i % k)
         runs = []
         for _ in range(5):
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record(stream)
             for i in range(20):
-                call(i % 3)
+                call(i % k)
             b.record(stream)
             b.synchronize()
             runs.append(a.elapsed_time(b) / 20)
@@ -547,37 +565,40 @@ def capi_rows(lib, impl: int, dev, stream) -> dict:
         out[f"{name}_capi_gbps"] = round(nbytes / (ms * 1e6), 1)
 
     strided = 1  # SPX_COLUMNS_STRIDED
+    k = rotation(64 << 20)  # C3's inputs: 64 MiB fields, 64.5 MiB spectra
     for n, arrays in ((128, 1024), (512, 64)):
-        xs = [torch.randn(arrays, n, n, device=dev, generator=g) for _ in range(3)]
+        xs = [torch.randn(arrays, n, n, device=dev, generator=g) for _ in range(k)]
         ys = [torch.empty(arrays, n, n // 2 + 1, dtype=torch.complex64, device=dev)
-              for _ in range(3)]
-        zs = [torch.empty(arrays, n, n, device=dev) for _ in range(3)]
+              for _ in range(k)]
+        zs = [torch.empty(arrays, n, n, device=dev) for _ in range(k)]
         w_f = workspace(lib.spx_fft2_r2c_workspace, impl, strided, n, n, arrays)
         w_i = workspace(lib.spx_fft2_c2r_workspace, impl, strided, n, n, arrays)
         torch.cuda.synchronize()
         work = fft2_real_work(n, n, arrays)[1]
         record(f"c3_rfft2_{n}", time_calls(lambda i: check(lib.spx_fft2_r2c(
             impl, strided, vp(xs[i].data_ptr()), vp(ys[i].data_ptr()), n, n, arrays,
-            vp(w_f.data_ptr()), sptr))), work)
+            vp(w_f.data_ptr()), sptr)), k), work)
         record(f"c3_irfft2_{n}", time_calls(lambda i: check(lib.spx_fft2_c2r(
             impl, strided, vp(ys[i].data_ptr()), vp(zs[i].data_ptr()), n, n, arrays,
-            vp(w_i.data_ptr()), sptr))), work)
+            vp(w_i.data_ptr()), sptr)), k), work)
         del xs, ys, zs, w_f, w_i
     # C4: [64, 32, 128, 128] <-> modes [64, 32, 32, 16], m1 = m2 = 16.
     arrays = 2048
-    xs = [torch.randn(arrays, 128, 128, device=dev, generator=g) for _ in range(3)]
-    ms = [torch.empty(arrays, 32, 16, dtype=torch.complex64, device=dev) for _ in range(3)]
-    zs = [torch.empty(arrays, 128, 128, device=dev) for _ in range(3)]
+    kf, ki = rotation(128 << 20), rotation(8 << 20)  # 128 MiB fields, 8 MiB of modes
+    xs = [torch.randn(arrays, 128, 128, device=dev, generator=g) for _ in range(kf)]
+    ms = [torch.randn(arrays, 32, 16, dtype=torch.complex64, device=dev, generator=g)
+          for _ in range(ki)]
+    zs = [torch.empty(arrays, 128, 128, device=dev) for _ in range(kf)]
     w_f = workspace(lib.spx_rfft2_modes_workspace, impl, 128, 128, 16, 16, arrays)
     w_i = workspace(lib.spx_irfft2_modes_workspace, impl, 128, 128, 16, 16, arrays)
     torch.cuda.synchronize()
     work = fft2_modes_work(128, 128, 16, 16, arrays)[1]
     record("c4_rfft2_modes_128_m16", time_calls(lambda i: check(lib.spx_rfft2_modes(
-        impl, vp(xs[i].data_ptr()), vp(ms[i].data_ptr()), 128, 128, 16, 16, arrays,
-        vp(w_f.data_ptr()), sptr))), work)
+        impl, vp(xs[i].data_ptr()), vp(ms[i % ki].data_ptr()), 128, 128, 16, 16, arrays,
+        vp(w_f.data_ptr()), sptr)), kf), work)
     record("c4_irfft2_modes_128_m16", time_calls(lambda i: check(lib.spx_irfft2_modes(
-        impl, vp(ms[i].data_ptr()), vp(zs[i].data_ptr()), 128, 128, 16, 16, arrays,
-        vp(w_i.data_ptr()), sptr))), work)
+        impl, vp(ms[i].data_ptr()), vp(zs[i % kf].data_ptr()), 128, 128, 16, 16, arrays,
+        vp(w_i.data_ptr()), sptr)), ki), work)
     return out
 
 

@@ -1,6 +1,7 @@
 """Builds the two shared libraries of the MI355X FFT stack, in-tree, for gfx950.
 
     python gpu-spectral-stack_amd/build.py [--jobs N] [--only capi|torch|tools] [--force]
+    python gpu-spectral-stack_amd/build.py --define NAME=VALUE [...] --lib-dir DIR
 
 1. libspectral_hip.so: every HIP kernel plus the C ABI of include/spectral_hip.h. Built with
    hipcc for --offload-arch=gfx950 only; depends on the HIP runtime and nothing from PyTorch.
@@ -127,6 +128,30 @@ def build_capi(jobs: int, force: bool = False) -> Path:
     return LIB
 
 
+def build_variant(jobs: int, defines: list[str], lib_dir: Path) -> Path:
+    """libspectral_hip.so built with extra -D definitions into lib_dir (its objects under
+    lib_dir/obj), for measuring a compile-time alternative next to the product library: the tools
+    pick it up through LD_LIBRARY_PATH (their RUNPATH gives way to it)."""
+    obj_dir = lib_dir / "obj"
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    flags = [*HIP_FLAGS, *[f"-D{d}" for d in defines]]
+
+    def compile_one(name: str) -> str:
+        src = CSRC / name
+        obj = obj_dir / (name + ".o")
+        lang = [] if src.suffix == ".hip" else ["-x", "hip"]
+        _run([HIPCC, *flags, *lang, "-c", str(src), "-o", str(obj)])
+        return str(obj)
+
+    print(f"  variant {' '.join(defines)} -> {lib_dir}", flush=True)
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(compile_one, CAPI_SOURCES))
+    lib = lib_dir / LIB.name
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(lib), *objs,
+          "-Wl,-soname,libspectral_hip.so"])
+    return lib
+
+
 def _torch_paths() -> tuple[list[str], list[str]]:
     import torch
     from torch.utils import cpp_extension
@@ -183,7 +208,15 @@ def main(argv: list[str] | None = None) -> None:
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
     ap.add_argument("--only", choices=["capi", "torch", "tools"])
     ap.add_argument("--force", action="store_true", help="recompile everything")
+    ap.add_argument("--define", action="append", default=[], metavar="NAME=VALUE",
+                    help="build only a variant library with this definition (repeatable)")
+    ap.add_argument("--lib-dir", type=Path, help="where the --define variant library goes")
     args = ap.parse_args(argv)
+    if args.define:
+        if args.lib_dir is None:
+            ap.error("--define needs --lib-dir")
+        build_variant(args.jobs, args.define, args.lib_dir.resolve())
+        return
     if args.only in (None, "capi"):
         build_capi(args.jobs, args.force)
     if args.only in (None, "torch"):

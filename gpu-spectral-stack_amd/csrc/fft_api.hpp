@@ -18,8 +18,12 @@ constexpr int kFourStepMaxN = kStockhamMaxN * kStockhamMaxN;  // 2^24 (reference
 // in one workgroup's LDS); the multi-pass splits take over beyond.
 constexpr int kSinglePassMaxN = 16384;
 // Above that, up to kTwoPassMaxN, a column pass and a row pass that stores transposed; beyond,
-// the column pass itself runs as two.
-constexpr int kTwoPassMaxN = 1 << 20;
+// the column pass itself runs as two. SPX_TWO_PASS_MAX_LOG2 overrides it in a variant build,
+// to measure the three-pass split at sizes the two-pass one serves.
+#ifndef SPX_TWO_PASS_MAX_LOG2
+#define SPX_TWO_PASS_MAX_LOG2 20
+#endif
+constexpr int kTwoPassMaxN = 1 << SPX_TWO_PASS_MAX_LOG2;
 
 // reference fft.hpp:14-15, 36-39, 59-60
 using C2cFn = void (*)(const cf32* x, cf32* y, int n, int batch, Direction direction,

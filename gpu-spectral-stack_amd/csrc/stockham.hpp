@@ -549,6 +549,78 @@ __device__ __forceinline__ constexpr int input_index(int lane, int b, int r)
     return lane + b * P::L + r * (P::N / P::template radix<S>());
 }
 
+// --- the exchange between two stages in registers ------------------------------------------
+//
+// A 64-point transform held by 8 lanes of 8 values in two radix-8 stages exchanges through an
+// 8 x 8 transpose: after stage 0, lane l holds elements 8 l .. 8 l + 7, and stage 1 needs
+// elements l, l + 8, .., l + 56. Three rounds of swaps between partner lanes l ^ 1, l ^ 2, l ^ 4
+// (each swapping the off-diagonal halves of 2 x 2 blocks of the lane x register matrix) do it
+// without LDS: DPP quad_perm moves a dword to the partner lane within a quad (^ 1, ^ 2), and
+// ds_swizzle in bit mode (and 0x1F, xor 4) across a quad pair (^ 4). Per lane that is 24 moves,
+// 24 DPP / swizzle ops and their selects, against 8 LDS writes and 8 LDS reads of 8 bytes.
+// It applies to transforms whose 8 lanes are 8 consecutive lanes of a wave in order
+// (lane = thread index mod 8, the row layout Padded), every lane of the group running it.
+//
+// Off by default: measured on MI355X against the LDS exchange (three alternated rounds at
+// 2^24 points, and SQ counters), it kept the same LDS instruction count (ds_write2 / ds_read2
+// move two values per instruction, and ds_swizzle is an LDS instruction too), raised VALU
+// instructions per wave by 18-40 % (C2C n = 64: 226 -> 316) and ran 2-9 % slower (R2C n = 128
+// 24.2 -> 26.7 us), irfft2 128^2 unchanged. Build with -DSPX_EXCHANGE_IN_REGISTERS=1 to
+// measure it (build.py --define SPX_EXCHANGE_IN_REGISTERS=1 --lib-dir DIR).
+#ifndef SPX_EXCHANGE_IN_REGISTERS
+#define SPX_EXCHANGE_IN_REGISTERS 0
+#endif
+constexpr bool kExchangeInRegisters = SPX_EXCHANGE_IN_REGISTERS != 0;
+
+template <class P, int S, class Lay>
+constexpr bool exchange_in_registers()
+{
+    return kExchangeInRegisters && std::is_same_v<Lay, Padded> && P::N == 64 && P::E == 8
+           && P::L == 8 && S == 0 && P::kStages == 2 && P::template radix<0>() == 8
+           && P::template radix<1>() == 8;
+}
+
+// One dword from the partner lane (lane ^ D) of the lane's group of 8.
+template <int D>
+__device__ __forceinline__ float from_partner(float x)
+{
+    const int i = __builtin_bit_cast(int, x);
+    if constexpr (D == 1) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false));
+    } else if constexpr (D == 2) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false));
+    } else {
+        static_assert(D == 4, "partners within groups of 8 lanes");
+        return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(i, 0x101F));
+    }
+}
+
+// Round D: lanes with bit D clear swap their registers r | D for the partner's registers r.
+template <int D>
+__device__ __forceinline__ void swap_with_partner(cf32 (&v)[8], int lane)
+{
+    const bool hi = (lane & D) != 0;
+    static_for<0, 8>([&](auto ri) {
+        constexpr int r0 = decltype(ri)::value;
+        if constexpr ((r0 & D) == 0) {
+            constexpr int r1 = r0 | D;
+            const cf32 send = hi ? v[r0] : v[r1];
+            const cf32 recv{from_partner<D>(send.re), from_partner<D>(send.im)};
+            v[r0] = hi ? recv : v[r0];
+            v[r1] = hi ? v[r1] : recv;
+        }
+    });
+}
+
+template <class P>
+__device__ __forceinline__ void transpose_lanes(cf32 (&v)[P::E], int lane)
+{
+    static_assert(P::E == 8 && P::L == 8, "an 8 x 8 transpose");
+    swap_with_partner<1>(v, lane);
+    swap_with_partner<2>(v, lane);
+    swap_with_partner<4>(v, lane);
+}
+
 // Runs stages S .. kStages-1. On entry v holds stage S's inputs; on exit the last stage's
 // outputs, output r of butterfly b being element lane + b L + r N / R_last.
 template <class P, int S, bool Inv, bool Table, class Lay = Padded>
@@ -556,10 +628,14 @@ __device__ __forceinline__ void run_stages(cf32 (&v)[P::E], cf32* s, int lane, c
 {
     stage_compute<P, S, Inv, Table>(v, lane, table);
     if constexpr (S + 1 < P::kStages) {
-        lds_sync<P::kWaveLocal>();  // every lane has read the previous contents of s
-        stage_write<P, S, Lay>(s, v, lane);
-        lds_sync<P::kWaveLocal>();
-        stage_read<P, S + 1, Lay>(s, v, lane);
+        if constexpr (exchange_in_registers<P, S, Lay>()) {
+            transpose_lanes<P>(v, lane);
+        } else {
+            lds_sync<P::kWaveLocal>();  // every lane has read the previous contents of s
+            stage_write<P, S, Lay>(s, v, lane);
+            lds_sync<P::kWaveLocal>();
+            stage_read<P, S + 1, Lay>(s, v, lane);
+        }
         run_stages<P, S + 1, Inv, Table, Lay>(v, s, lane, table);
     }
 }
@@ -1046,8 +1122,15 @@ struct R2cIoT {
     template <class P>
     static constexpr bool direct_out() { return false; }
 
+    // Nontemporal loads: with the inputs in rotation beyond the Infinity Cache (twice its size),
+    // three alternated A/B rounds at 2^24 points on MI355X ran n = 16 .. 1024 1-2.4 % faster than
+    // plain loads (n = 1024: 24.97 -> 24.37 us) and no size slower. (Plain loads had looked
+    // faster when the inputs of a three-set rotation could stay in that cache.)
     template <class P>
-    __device__ __forceinline__ cf32 in(long long t, int i) const { return z[t * P::N + i]; }
+    __device__ __forceinline__ cf32 in(long long t, int i) const
+    {
+        return ld_stream(z + t * P::N + i);
+    }
     template <class P>
     __device__ __forceinline__ void out(long long, int, cf32) const {}
 
@@ -1058,7 +1141,7 @@ struct R2cIoT {
         const cf32* src = z + first * P::N;
         cf32 val[S::kSteps];
         S::each(count, tid, [&](int k, int u, int i, bool valid) {
-            val[k] = valid ? src[u * P::N + i] : czero();
+            val[k] = valid ? ld_stream(src + u * P::N + i) : czero();
         });
         S::each(count, tid, [&](int k, int u, int i, bool valid) {
             if (valid) {
@@ -1203,10 +1286,15 @@ struct C2rIo {
         static_assert(pad(m) < P::kStride, "a row of m + 1 values fits its LDS stride");
         // The half spectrum X[0 .. m] into LDS (zero beyond keep).
         using H = Staged<G, m + 1>;
+        // Nontemporal loads for m <= 32, plain beyond: with cache-clean inputs (three alternated
+        // A/B rounds at 2^24 points) nontemporal loads ran n = 8 .. 64 0.2-5 % faster and
+        // n = 1024 and 4096 about 2 % slower.
         const cf32* src = x + first * keep;
         cf32 val[H::kSteps];
         H::each(count, tid, [&](int j, int u, int k, bool valid) {
-            val[j] = (valid && k < keep) ? src[u * keep + k] : czero();
+            val[j] = (valid && k < keep)
+                         ? (m <= 32 ? ld_stream(src + u * keep + k) : src[u * keep + k])
+                         : czero();
         });
         H::each(count, tid, [&](int j, int u, int k, bool valid) {
             if (valid) {

@@ -109,7 +109,9 @@ __global__ void __launch_bounds__(Th) rows_copy_kernel(const f2v* __restrict__ i
 
 // Uneven mixes: workgroup b reads Th * V contiguous values as rows_copy_kernel does and writes
 // Th of them (each lane the sum of its V), or the mirror (Expand: reads Th, writes each V times).
-// V = 16 is the byte mix of a pruned 2D transform keeping a sixteenth of its input (C4).
+// V = 16 is the byte mix of a pruned 2D transform keeping a sixteenth of its input (C4), V = 2
+// that of the real transforms at n = 2 (C2), V = 1 an even copy with plain loads and nontemporal
+// stores, as the real transforms access memory.
 template <int Th, int V, bool Expand>
 __global__ void __launch_bounds__(Th) mix_rows_kernel(const f2v* __restrict__ in, f2v* __restrict__ out)
 {
@@ -242,7 +244,7 @@ float median(std::vector<float> v)
 }
 
 // --patterns: each pattern copies `values` 8-byte values (in + out = 16 bytes per value) from
-// one buffer of a rotating set of four into another (1-2 GiB in all, beyond the 256 MB cache);
+// one buffer of a rotating set of eight into another (2 GiB in all, beyond the 256 MB cache);
 // the patterns run interleaved over 7 rounds of 20 launches and each reports its median round.
 struct Pattern {
     const char* name;
@@ -304,6 +306,12 @@ int run_patterns()
          [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, true>(k2e23, i, o, s); }, {}},
         {"rows 16 KB chunks, plain", "C3 512^2 row-pair pass (2^23 values)", k2e23,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, false>(k2e23, i, o, s); }, {}},
+        {"rows, plain loads, nontemporal stores", "C2 R2C / C2R n = 8 .. 4096 (64 + 64 MiB)", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 1, false>(k2e23, i, o, s); }, {}},
+        {"rows, 2 B read per 1 B written", "C2 C2R n = 2: 128 MiB in, 64 MiB out", (k2e24 + k2e24 / 2) / 2,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 2, false>(k2e24, i, o, s); }, {}},
+        {"rows, 1 B read per 2 B written", "C2 R2C n = 2: 64 MiB in, 128 MiB out", (k2e24 + k2e24 / 2) / 2,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 2, true>(k2e24, i, o, s); }, {}},
         {"rows, 16 B read per 1 B written", "C4 rfft2_modes: 128 MiB in, 8 MiB out", (k2e24 + k2e24 / 16) / 2,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 16, false>(k2e24, i, o, s); }, {}},
         {"rows, 1 B read per 16 B written", "C4 irfft2_modes: 8 MiB in, 128 MiB out", (k2e24 + k2e24 / 16) / 2,
@@ -331,7 +339,9 @@ int run_patterns()
         {"tiles 16 x 1024 of 1024 x 1024, plain", "128-byte runs", k2e24,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_tiles<1024, 1024, 16, 1024, false>(k2e24, i, o, s); }, {}},
     };
-    constexpr int kSets = 4;
+    // Eight sets: the smallest inputs here (2^23 values, 64 MiB) then total 512 MiB in rotation,
+    // twice the Infinity Cache, so no launch reads what an earlier one left there.
+    constexpr int kSets = 8;
     const std::size_t bytes = k2e24 * sizeof(f2v);
     f2v* in[kSets];
     f2v* out[kSets];
