@@ -130,8 +130,19 @@ def test_workspace_queries(lib):
     count = ctypes.c_size_t()
     assert lib.spx_fft2_c2c_workspace(3, 1, 8, 8, 2, ctypes.byref(count)) == SPX_OK
     assert count.value == 0
+    # The transpose method: the Stockham implementations' two passes go through one array-sized
+    # region (n2 x n1, or (n2/2 + 1) x n1 for real transforms); naive's four kernels through two,
+    # plus its real-row scratch; a side of 1 or real rows of 2 take the four-kernel route too.
     assert lib.spx_fft2_c2c_workspace(3, 0, 8, 8, 2, ctypes.byref(count)) == SPX_OK
-    assert count.value == 2 * 8 * 8 * 2
+    assert count.value == 8 * 8 * 2
+    assert lib.spx_fft2_r2c_workspace(3, 0, 8, 8, 2, ctypes.byref(count)) == SPX_OK
+    assert count.value == 8 * 5 * 2
+    assert lib.spx_fft2_c2r_workspace(1, 0, 16, 32, 3, ctypes.byref(count)) == SPX_OK
+    assert count.value == 16 * 17 * 3
+    assert lib.spx_fft2_c2c_workspace(3, 0, 1, 8, 2, ctypes.byref(count)) == SPX_OK
+    assert count.value == 2 * 1 * 8 * 2
+    assert lib.spx_fft2_r2c_workspace(4, 0, 8, 2, 2, ctypes.byref(count)) == SPX_OK
+    assert count.value == 2 * 8 * 2 * 2
     assert lib.spx_fft2_r2c_workspace(0, 0, 8, 8, 2, ctypes.byref(count)) == SPX_OK
     assert count.value == 2 * 8 * 5 * 2 + 8 * 4 * 2
     # 128 x 128 runs as one single-pass kernel (no workspace); 512 x 512 as rows then columns,
