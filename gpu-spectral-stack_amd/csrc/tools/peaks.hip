@@ -91,8 +91,9 @@ __device__ __forceinline__ void store8(f2v* p, f2v v)
 }
 
 // Contiguous rows: workgroup b copies the Th * V 8-byte values from b Th V, lane t taking values
-// t + k Th (runs of 512 bytes per wave access). The grid covers the buffer exactly.
-template <int Th, int V, bool NT>
+// t + k Th (runs of 512 bytes per wave access). The grid covers the buffer exactly. NT: both
+// accesses nontemporal; StoreNT (default NT): the stores' hint on its own.
+template <int Th, int V, bool NT, bool StoreNT = NT>
 __global__ void __launch_bounds__(Th) rows_copy_kernel(const f2v* __restrict__ in, f2v* __restrict__ out)
 {
     const std::size_t base = static_cast<std::size_t>(blockIdx.x) * Th * V + threadIdx.x;
@@ -103,7 +104,7 @@ __global__ void __launch_bounds__(Th) rows_copy_kernel(const f2v* __restrict__ i
     }
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-        store8<NT>(out + base + static_cast<std::size_t>(k) * Th, v[k]);
+        store8<StoreNT>(out + base + static_cast<std::size_t>(k) * Th, v[k]);
     }
 }
 
@@ -135,6 +136,22 @@ __global__ void __launch_bounds__(Th) mix_rows_kernel(const f2v* __restrict__ in
             sum += v[k];
         }
         store8<true>(out + narrow, sum);
+    }
+}
+
+// The same 2:1 and 1:2 mixes with one 16-byte access per lane, the way the n = 2 real
+// transforms move their rows (a row of two complex values is 16 bytes): Expand reads 8 bytes and
+// writes 16, else reads 16 and writes 8. Plain loads, nontemporal stores.
+template <int Th, bool Expand>
+__global__ void __launch_bounds__(Th) mix16_kernel(const f2v* __restrict__ in, f2v* __restrict__ out)
+{
+    const std::size_t i = static_cast<std::size_t>(blockIdx.x) * Th + threadIdx.x;
+    if constexpr (Expand) {
+        const f2v v = in[i];
+        __builtin_nontemporal_store(f4v{v.x, v.y, v.y, v.x}, reinterpret_cast<f4v*>(out) + i);
+    } else {
+        const f4v v = reinterpret_cast<const f4v*>(in)[i];
+        store8<true>(out + i, f2v{v.x + v.z, v.y + v.w});
     }
 }
 
@@ -254,11 +271,11 @@ struct Pattern {
     std::vector<float> us;
 };
 
-template <int Th, int V, bool NT>
+template <int Th, int V, bool NT, bool StoreNT = NT>
 void launch_rows(std::size_t values, const f2v* in, f2v* out, hipStream_t s)
 {
-    hipLaunchKernelGGL((rows_copy_kernel<Th, V, NT>), dim3(static_cast<unsigned>(values / (Th * V))),
-                       dim3(Th), 0, s, in, out);
+    hipLaunchKernelGGL((rows_copy_kernel<Th, V, NT, StoreNT>),
+                       dim3(static_cast<unsigned>(values / (Th * V))), dim3(Th), 0, s, in, out);
 }
 
 template <int Rows, int Cols, int T, int Th, bool NT>
@@ -292,6 +309,13 @@ void launch_mix(std::size_t wide_values, const f2v* in, f2v* out, hipStream_t s)
                        dim3(static_cast<unsigned>(wide_values / (Th * V))), dim3(Th), 0, s, in, out);
 }
 
+template <int Th, bool Expand>
+void launch_mix16(std::size_t rows, const f2v* in, f2v* out, hipStream_t s)
+{
+    hipLaunchKernelGGL((mix16_kernel<Th, Expand>), dim3(static_cast<unsigned>(rows / Th)), dim3(Th),
+                       0, s, in, out);
+}
+
 constexpr std::size_t k2e24 = std::size_t(1) << 24;
 constexpr std::size_t k2e23 = std::size_t(1) << 23;
 
@@ -306,12 +330,18 @@ int run_patterns()
          [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, true>(k2e23, i, o, s); }, {}},
         {"rows 16 KB chunks, plain", "C3 512^2 row-pair pass (2^23 values)", k2e23,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, false>(k2e23, i, o, s); }, {}},
-        {"rows, plain loads, nontemporal stores", "C2 R2C / C2R n = 8 .. 4096 (64 + 64 MiB)", k2e23,
+        {"rows 16 KB chunks, plain loads, nontemporal stores", "C2 R2C / C2R n = 8 .. 4096 (64 + 64 MiB)", k2e23,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, false, true>(k2e23, i, o, s); }, {}},
+        {"rows 2 KB chunks, plain loads, nontemporal stores", "the same, one value per lane", k2e23,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 1, false>(k2e23, i, o, s); }, {}},
         {"rows, 2 B read per 1 B written", "C2 C2R n = 2: 128 MiB in, 64 MiB out", (k2e24 + k2e24 / 2) / 2,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 2, false>(k2e24, i, o, s); }, {}},
         {"rows, 1 B read per 2 B written", "C2 R2C n = 2: 64 MiB in, 128 MiB out", (k2e24 + k2e24 / 2) / 2,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 2, true>(k2e24, i, o, s); }, {}},
+        {"rows, 16-byte loads, 8-byte stores (2:1)", "C2 C2R n = 2, as its kernel moves rows", (k2e24 + k2e24 / 2) / 2,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_mix16<256, false>(k2e23, i, o, s); }, {}},
+        {"rows, 8-byte loads, 16-byte stores (1:2)", "C2 R2C n = 2, as its kernel moves rows", (k2e24 + k2e24 / 2) / 2,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_mix16<256, true>(k2e23, i, o, s); }, {}},
         {"rows, 16 B read per 1 B written", "C4 rfft2_modes: 128 MiB in, 8 MiB out", (k2e24 + k2e24 / 16) / 2,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_mix<256, 16, false>(k2e24, i, o, s); }, {}},
         {"rows, 1 B read per 16 B written", "C4 irfft2_modes: 8 MiB in, 128 MiB out", (k2e24 + k2e24 / 16) / 2,
