@@ -1094,17 +1094,19 @@ struct R2cIoT {
     // The group's rows leave LDS as one run in whole 128-byte lines (store_run_aligned): rows of
     // m + 1 values start at 8-byte offsets, and stores that straddle lines wrote 5-9 % more bytes
     // than the output holds (WRITE_SIZE, n = 128 .. 8192); in whole lines, 0.2-1.8 %. Rows of
-    // fewer than 64 lanes are staged through LDS anyway. Rows of 64 lanes or more take it when
-    // their plan has radix 8 or more and at most 8 values per lane (15 interleaved rounds at
-    // radix 8: n = 1024 69.9 -> 72.8 %, 2048 68.5 -> 75.1 %, 4096 70.5 -> 77.2 % of 8 TB/s);
+    // fewer than 64 lanes are staged through LDS anyway. Rows of exactly 64 lanes take it when
+    // their plan has radix 8 or more and at most 8 values per lane (radix 8, n = 1024: 24.54
+    // against 26.25 us for the direct store, four alternated rounds with cache-clean inputs);
     // the other plans store their bins X[k] straight from registers, runs of L values, where
-    // the extra LDS pass cost more than it saved (n = 8192 at 16 values per lane 67.8 -> 64.6 %,
-    // radix 4 at n = 1024 73.5 -> 67.0 %). Aligned = false keeps the direct store for every row
-    // of 64 lanes or more and the row-by-row staged store for the others.
+    // the extra LDS pass cost more than it saved: n = 2048 (128 lanes) 29.20 -> 27.35 us in the
+    // same rounds, n = 4096 (256 lanes) equal, n = 8192 at 16 values per lane 67.8 -> 64.6 % and
+    // radix 4 at n = 1024 73.5 -> 67.0 % of 8 TB/s in earlier interleaved rounds. Aligned = false
+    // keeps the direct store for every row of 64 lanes or more and the row-by-row staged store
+    // for the others.
     template <class P>
     static constexpr bool aligned_store()
     {
-        return Aligned && (P::L < 64 || (P::R >= 8 && P::E <= 8));
+        return Aligned && (P::L < 64 || (P::L == 64 && P::R >= 8 && P::E <= 8));
     }
     template <class P>
     static constexpr bool direct_store() { return !aligned_store<P>() && P::L >= 64; }
