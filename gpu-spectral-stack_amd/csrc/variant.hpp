@@ -131,6 +131,31 @@ void launch_columns_persistent(const StridedIo& io, long long batch, hipStream_t
     SPX_LAUNCH_CHECK();
 }
 
+// A persistent kernel whose workgroup g takes items g, g + G, ... of `items`: G = the workgroups
+// that fit on the device at once (at most `items`). Kernel arguments follow `stream`.
+template <class... KArgs, class... Args>
+void launch_persistent(void (*kernel)(KArgs...), int threads, long long items,
+                       hipStream_t stream, Args... args)
+{
+    static const int per_cu = [kernel, threads] {
+        int blocks = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &blocks, reinterpret_cast<const void*>(kernel), threads, 0);
+        return e == hipSuccess && blocks > 0 ? blocks : 1;
+    }();
+    const long long grid = std::min(items, static_cast<long long>(device_cus()) * per_cu);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(threads), 0, stream,
+                       args...);
+    SPX_LAUNCH_CHECK();
+}
+
+// The single-pass irfft2 of one array per workgroup runs persistent (the next array's loads
+// overlap the current one's row pass and stores); 0 keeps one array per workgroup.
+#ifndef SPX_FUSED_PERSISTENT
+#define SPX_FUSED_PERSISTENT 1
+#endif
+inline constexpr bool kFusedPersistent = SPX_FUSED_PERSISTENT != 0;
+
 // Strided columns of 256, 512 and 1024 points, and of 64 and 128 points in wide matrices, run
 // persistent (columns_kernel); other lengths keep one tile per workgroup. The 1024-point tiles hold
 // 8 columns of 16 values per lane, one wave per column (workgroups of 512 lanes), in XCD order:
@@ -716,8 +741,9 @@ struct Stockham {
     }
 
     // Columns of n = 2048 or 4096 points as two passes of 64 x (n / 64) (a four-step split of
-    // the column axis): a single pass would stage only 4 or 2 columns per workgroup, reading runs of 32 or
-    // 16 bytes; each of these passes stages 32 columns of 64 points (256-byte runs). Pass A runs
+    // the column axis): a single pass would stage only 4 or 2 columns per workgroup, reading
+    // runs of 32 or 16 bytes; each of these passes stages 32 columns of 64 points (256-byte
+    // runs). Pass A runs
     // the 64-point transforms over rows j1 (n/64) + j2 and twiddles them (x -> work); pass B runs
     // the (n/64)-point transforms over rows k1 (n/64) + j2 and writes row k1 + 64 k2 (work -> y).
     static void long_columns(const cf32* x, cf32* y, int n, int cols, int slabs,
@@ -1048,6 +1074,14 @@ struct Fused2dDriver {
         using F = dev::Fused2d<N1, M, R, Table>;
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
         const cf32* table = Table ? twiddle_table() : nullptr;
+        if constexpr (F::AP == 1 && dev::kFusedPersistent && dev::FullRows<F>::kUse) {
+            if (m1 == 0 && w == M + 1) {
+                dev::launch_persistent(dev::irfft2_full_persistent_kernel<F>, F::NT, batch,
+                                       stream, x, reinterpret_cast<cf32*>(y),
+                                       static_cast<long long>(batch), table);
+                return;
+            }
+        }
         const int rows_in = m1 > 0 ? 2 * m1 : N1;
         const auto kernel = (m1 == 0 && w == M + 1) ? dev::irfft2_fused_kernel<F, true>
                                                     : dev::irfft2_fused_kernel<F, false>;

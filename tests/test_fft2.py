@@ -176,6 +176,35 @@ def test_single_pass_rfft2_and_irfft2(rng, impl, n1, n2):
     assert_transform_close(back, ref.irfft2(spectrum, (n1, n2)), n1 * n2, axes=AXES)
 
 
+# The whole-spectrum irfft2 of 16384-point arrays runs persistent: workgroup g transforms arrays
+# g, g + G, g + 2G, ... (G = the workgroups resident at once, 512 on a 256-CU MI355X). 1283 arrays
+# take the loop round three times, the third time for only some workgroups. Arrays on either side
+# of each turn are checked against the oracle; every array's forward (one array per workgroup,
+# 1283 workgroups) against torch.fft (rocFFT), and its inverse through the round trip.
+PERSISTENT_SHAPES = [(128, 128), (256, 64), (64, 256)]
+TURN_EDGES = [0, 1, 511, 512, 513, 1023, 1024, 1025, 1281, 1282]
+
+
+@pytest.mark.parametrize("impl", FUSED_IMPLS)
+@pytest.mark.parametrize(("n1", "n2"), PERSISTENT_SHAPES)
+def test_single_pass_real_2d_over_more_arrays_than_resident_workgroups(rng, impl, n1, n2):
+    batch, n = 1283, n1 * n2
+    x = random_real(rng, (batch, n1, n2))
+    xd = dev(x)
+    y = spectral.rfft2(xd, impl=impl)
+    assert_transform_close(y[TURN_EDGES].cpu().numpy(), ref.rfft2(x[TURN_EDGES]), n, axes=AXES)
+    assert_transform_close(y.cpu().numpy(), torch.fft.rfft2(xd).cpu().numpy(), n, axes=AXES,
+                           tol=2 * fft_tolerance(n))
+    back = spectral.irfft2(y, n2, impl=impl)
+    assert_transform_close(back.cpu().numpy(), x, n, axes=AXES, tol=2 * fft_tolerance(n))
+
+    # A general half spectrum (not one of a real field) at the turn edges.
+    spectrum = random_complex(rng, (batch, n1, n2 // 2 + 1))
+    field = spectral.irfft2(dev(spectrum), n2, impl=impl)
+    assert_transform_close(field[TURN_EDGES].cpu().numpy(),
+                           ref.irfft2(spectrum[TURN_EDGES], (n1, n2)), n, axes=AXES)
+
+
 # Shapes past the single-pass kernels with n2 >= 32 run column-first: columns over the real array
 # read as complex, then one pass over pairs of rows (k1, -k1). n1 = 1 and 2 make every row its own
 # partner; batches of 3 leave the last workgroup's pairs partly empty. The inverse takes random,
