@@ -606,8 +606,9 @@ def radio_rows(impl: str, dev, later: list) -> dict:
     """spectral.rf as the reference's bench/bench_rf.py times it: 2^22 complex64 samples from
     seed 0, FIR of 63 and 1025 random taps (default block sizes 256 and 4096), and the Hann
     spectrum of 1024-sample frames; effective GB/s counts 16 bytes per sample (each read and
-    written once). The same operations composed on torch.fft are timed by what this appends to
-    `later`."""
+    written once). One signal is 32 MiB, so the calls rotate over `rotation()` signals (512 MiB)
+    and none reads a signal an earlier call left in the Infinity Cache. The same operations
+    composed on torch.fft are timed by what this appends to `later`."""
     import torch
 
     from spectral import rf
@@ -615,7 +616,14 @@ def radio_rows(impl: str, dev, later: list) -> dict:
 
     g = torch.Generator(device=dev).manual_seed(0)
     n = 1 << 22
-    x = torch.randn(n, dtype=torch.complex64, device=dev, generator=g)
+    xs = [torch.randn(n, dtype=torch.complex64, device=dev, generator=g)
+          for _ in range(rotation(8 * n))]
+    turn = [0]
+
+    def signal():
+        turn[0] += 1
+        return xs[turn[0] % len(xs)]
+
     out = {}
 
     theirs = []
@@ -628,11 +636,11 @@ def radio_rows(impl: str, dev, later: list) -> dict:
 
     for m in (63, 1025):
         taps = torch.randn(m, device=dev, generator=g)
-        record(f"rf_fir{m}_2e22", lambda t=taps: rf.fir(x, t, fft_impl=impl),
-               lambda t=taps: rf.fir(x, t, fft_impl="rocfft"))
+        record(f"rf_fir{m}_2e22", lambda t=taps: rf.fir(signal(), t, fft_impl=impl),
+               lambda t=taps: rf.fir(signal(), t, fft_impl="rocfft"))
     record("rf_spectrum1024_hann_2e22",
-           lambda: rf.spectrum(x, 1024, window_name="hann", fft_impl=impl),
-           lambda: rf.spectrum(x, 1024, window_name="hann", fft_impl="rocfft"))
+           lambda: rf.spectrum(signal(), 1024, window_name="hann", fft_impl=impl),
+           lambda: rf.spectrum(signal(), 1024, window_name="hann", fft_impl="rocfft"))
     later.append(lambda: {key: round(time_gpu(fn).median_ms, 5) for key, fn in theirs})
     return out
 
