@@ -132,19 +132,20 @@ void launch_columns_persistent(const StridedIo& io, long long batch, hipStream_t
 }
 
 // A persistent kernel whose workgroup g takes items g, g + G, ... of `items`: G = the workgroups
-// that fit on the device at once (at most `items`). Kernel arguments follow `stream`.
-template <class... KArgs, class... Args>
-void launch_persistent(void (*kernel)(KArgs...), int threads, long long items,
-                       hipStream_t stream, Args... args)
+// that fit on the device at once (at most `items`). The workgroups per CU are queried once per
+// kernel (a template argument, so kernels of one signature keep their own count). Kernel
+// arguments follow `stream`.
+template <auto Kernel, class... Args>
+void launch_persistent(int threads, long long items, hipStream_t stream, Args... args)
 {
-    static const int per_cu = [kernel, threads] {
+    static const int per_cu = [threads] {
         int blocks = 0;
         const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &blocks, reinterpret_cast<const void*>(kernel), threads, 0);
+            &blocks, reinterpret_cast<const void*>(Kernel), threads, 0);
         return e == hipSuccess && blocks > 0 ? blocks : 1;
     }();
     const long long grid = std::min(items, static_cast<long long>(device_cus()) * per_cu);
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(threads), 0, stream,
+    hipLaunchKernelGGL(Kernel, dim3(static_cast<unsigned>(grid)), dim3(threads), 0, stream,
                        args...);
     SPX_LAUNCH_CHECK();
 }
@@ -1076,9 +1077,9 @@ struct Fused2dDriver {
         const cf32* table = Table ? twiddle_table() : nullptr;
         if constexpr (F::AP == 1 && dev::kFusedPersistent && dev::FullRows<F>::kUse) {
             if (m1 == 0 && w == M + 1) {
-                dev::launch_persistent(dev::irfft2_full_persistent_kernel<F>, F::NT, batch,
-                                       stream, x, reinterpret_cast<cf32*>(y),
-                                       static_cast<long long>(batch), table);
+                dev::launch_persistent<dev::irfft2_full_persistent_kernel<F>>(
+                    F::NT, batch, stream, x, reinterpret_cast<cf32*>(y),
+                    static_cast<long long>(batch), table);
                 return;
             }
         }
