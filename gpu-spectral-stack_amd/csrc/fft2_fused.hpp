@@ -43,6 +43,24 @@ struct FastDiv {
     __device__ __forceinline__ unsigned div(unsigned x) const { return __umulhi(x << 1, m); }
 };
 
+// Values per lane of the single-pass kernels' column transforms: 16 from 128 rows on.
+template <int N1, int R>
+constexpr int column_values()
+{
+    return N1 >= 128 ? cmax(16, default_e<N1, R>()) : default_e<N1, R>();
+}
+
+// Their radix. Where a lane holds 16 values, the radix-8 variants run radix-16 stages: 128 rows
+// as 16 x 8 (one LDS exchange and one twiddle stage, against 8 x 8 x 2's two of each), 256 as
+// 16 x 16. Measured at 128 x 128 x 1024 (four alternated rounds, one box): rfft2 32.35 -> 31.08
+// us, irfft2 34.79 -> 31.28 us; and at C4's 2048 arrays of 128 x 128 (m = 16), 29.05 -> 28.84
+// and 28.58 -> 28.23 us.
+template <int N1, int R>
+constexpr int column_radix()
+{
+    return (R == 8 && column_values<N1, R>() >= 16) ? 16 : R;
+}
+
 template <int N1_, int M_, int R, bool Table, int BudgetKB = 80, int Threads = 512>
 struct Fused2d {
     static constexpr int N1 = N1_;                 // rows (column transform length)
@@ -52,8 +70,9 @@ struct Fused2d {
     using PR = Plan<M, R, default_e<M, R>()>;     // row transforms
     // Column transforms: 16 values per lane from 128 rows, so a 512-lane workgroup covers 64
     // columns per pass (65 columns of a 128 x 128 half spectrum in two passes, not three);
-    // measured 5-9 % faster at 128 x 128, neutral at 64 x 64.
-    using PC = Plan<N1, R, (N1 >= 128 ? cmax(16, default_e<N1, R>()) : default_e<N1, R>())>;
+    // measured 5-9 % faster at 128 x 128, neutral at 64 x 64. With 16 values per lane the
+    // radix-8 variants take radix-16 stages (column_radix).
+    using PC = Plan<N1, column_radix<N1, R>(), column_values<N1, R>()>;
     // Tile layout: row f, column c of array a at tile[a kTile + row_at(f) + pad(c)]. A tile row
     // holds pad(M) + 1 values (a padded row transform, or the M + 1 bins). One array per
     // workgroup with rows of 64 complex values or more (128 x 128): row f in tile row pad(f),

@@ -30,7 +30,7 @@ struct Modes2d {
     static constexpr bool kTable = Table;
     static constexpr int WMax = M / 4;  // kept columns this kernel takes
     using PR = Plan<M, R, default_e<M, R>()>;
-    using PC = Plan<N1, R, (N1 >= 128 ? cmax(16, default_e<N1, R>()) : default_e<N1, R>())>;
+    using PC = Plan<N1, column_radix<N1, R>(), column_values<N1, R>()>;  // as Fused2d's
     static constexpr int NT = 256;
     static constexpr int RPP = NT / PR::L;        // rows per pass
     static constexpr int kPasses = N1 / RPP;
