@@ -902,4 +902,98 @@ __global__ void __launch_bounds__(F::NT)
     }
 }
 
+// Persistent complex 2D for one array per workgroup whose rows load straight from HBM (fft2 /
+// ifft2 of 128 x 128: a 140 KB tile, one workgroup per CU, so no other workgroup's traffic
+// overlaps its LDS phases). Workgroup g takes arrays g, g + G, ...: every row pass's loads are
+// issued before the first pass's transform, and the next array's rows are issued once the
+// current array's rows are in the tile, so they are in flight during its column pass and
+// stores. The wave waits for them, with its stores, at the top of the next turn.
+template <class F, bool Inv>
+__global__ void __launch_bounds__(F::NT)
+    fft2_full_persistent_kernel(const cf32* __restrict__ x, cf32* __restrict__ y,
+                                long long batch, float scale, const cf32* table)
+{
+    static_assert(F::AP == 1 && F::PR::L >= 16, "one array per workgroup, rows loaded directly");
+    using PR = typename F::PR;
+    using PC = typename F::PC;
+    __shared__ cf32 tile[F::kTile];
+    constexpr int kPerArray = F::N1 * F::M;
+    constexpr int kPasses = F::N1 / F::RPP;
+    constexpr int R0 = PR::template radix<0>();
+    static_assert(kPasses * PR::E <= 32, "all row passes' inputs fit in registers");
+
+    cf32 v[kPasses][PR::E];
+    const auto fetch = [&](long long a, int tid) __attribute__((always_inline)) {
+        const int lane = tid % PR::L;
+        static_for<0, kPasses>([&](auto pi) {
+            constexpr int p = decltype(pi)::value;
+            const cf32* const src = x + (a * F::N1 + p * F::RPP + tid / PR::L) * F::M;
+#pragma unroll
+            for (int b = 0; b < PR::E / R0; ++b) {
+#pragma unroll
+                for (int r = 0; r < R0; ++r) {
+                    v[p][b * R0 + r] = ld_stream(src + input_index<PR, 0>(lane, b, r));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
+    long long a = blockIdx.x;
+    fetch(a, threadIdx.x);
+#pragma unroll 1
+    for (; a < batch; a += gridDim.x) {
+        const int tid = opaque_tid<F::NT>();
+        {
+            const int lane = tid % PR::L;
+            static_for<0, kPasses>([&](auto pi) {
+                constexpr int p = decltype(pi)::value;
+                cf32* const s = tile + F::row_at(p * F::RPP + tid / PR::L);
+                run_stages<PR, 0, Inv, F::kTable>(v[p], s, lane, table);
+                lds_sync<true>();
+                final_write<PR>(s, v[p], lane);
+            });
+        }
+        __syncthreads();
+        const long long next = a + gridDim.x;
+        if (next < batch) {
+            fetch(next, tid);
+        }
+
+#pragma unroll 1
+        for (int c0 = 0; c0 < F::M; c0 += F::CPP) {
+            const int c = c0 + F::col_slot(tid);
+            if (c < F::M) {
+                cf32* const s = tile + pad(c);
+                const int cl = F::col_lane(tid);
+                cf32 u[PC::E];
+                stage_read<PC, 0, typename F::ColLay>(s, u, cl);
+                run_stages<PC, 0, Inv, F::kTable, typename F::ColLay>(u, s, cl, table);
+                lds_sync<true>();
+                final_write<PC, typename F::ColLay>(s, u, cl);
+            }
+        }
+        __syncthreads();
+
+        cf32* const dst = y + a * kPerArray;
+        constexpr int kStoreChunk = 8;
+        static_assert(kPerArray % (F::NT * kStoreChunk) == 0, "whole store steps");
+#pragma unroll 1
+        for (int e0 = 0; e0 < kPerArray; e0 += F::NT * kStoreChunk) {
+            cf32 val[kStoreChunk];
+#pragma unroll
+            for (int k = 0; k < kStoreChunk; ++k) {
+                const int e = e0 + k * F::NT + tid;
+                const int f = e / F::M;
+                val[k] = tile[F::row_at(f) + pad(e - f * F::M)];
+            }
+#pragma unroll
+            for (int k = 0; k < kStoreChunk; ++k) {
+                st_stream(dst + e0 + k * F::NT + tid, cscale(val[k], scale));
+            }
+        }
+        __syncthreads();  // the next array's rows overwrite the tile
+    }
+}
+
 }  // namespace spx::dev

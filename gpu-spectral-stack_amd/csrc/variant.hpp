@@ -166,8 +166,8 @@ void launch_persistent(int threads, long long items, hipStream_t stream, Args...
     SPX_LAUNCH_CHECK();
 }
 
-// The single-pass irfft2 of one array per workgroup runs persistent (the next array's loads
-// overlap the current one's row pass and stores); 0 keeps one array per workgroup.
+// The single-pass irfft2 and the complex fft2 of one array per workgroup run persistent (the
+// next array's loads overlap the current one's later phases); 0 keeps one array per workgroup.
 #ifndef SPX_FUSED_PERSISTENT
 #define SPX_FUSED_PERSISTENT 1
 #endif
@@ -1154,6 +1154,16 @@ struct Fused2dDriver {
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
         const cf32* table = Table ? twiddle_table() : nullptr;
         const float scale = inverse ? 1.0f / static_cast<float>(N1 * N2) : 1.0f;
+        if constexpr (F::AP == 1 && F::PR::L >= 16 && dev::kFusedPersistent) {
+            if (inverse) {
+                dev::launch_persistent<dev::fft2_full_persistent_kernel<F, true>>(
+                    F::NT, batch, stream, x, y, static_cast<long long>(batch), scale, table);
+            } else {
+                dev::launch_persistent<dev::fft2_full_persistent_kernel<F, false>>(
+                    F::NT, batch, stream, x, y, static_cast<long long>(batch), scale, table);
+            }
+            return;
+        }
         if (inverse) {
             hipLaunchKernelGGL((dev::fft2_fused_kernel<F, true>),
                                dim3(static_cast<unsigned>(blocks)), dim3(F::NT), 0, stream, x, y,

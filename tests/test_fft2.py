@@ -247,6 +247,20 @@ def test_single_pass_fft2_and_ifft2(rng, impl, n1, n2):
     assert_transform_close(back, ref.ifft2(x), n1 * n2, axes=AXES)
 
 
+# The single-pass complex 2D of 16384-point arrays runs persistent: workgroup g transforms arrays
+# g, g + G, ... (G = the workgroups resident at once: one per CU at 128 x 128, two at 64 x 128).
+# The batches take the loop round three times, the third time for only some workgroups; every
+# array is checked against the oracle in both directions.
+@pytest.mark.parametrize("impl", FUSED_IMPLS)
+@pytest.mark.parametrize(("n1", "n2", "batch"), [(128, 128, 600), (64, 128, 1283)])
+def test_single_pass_fft2_over_more_arrays_than_resident_workgroups(rng, impl, n1, n2, batch):
+    x = random_complex(rng, (batch, n1, n2))
+    y = spectral.fft2(dev(x), impl=impl)
+    assert_transform_close(y, ref.fft2(x), n1 * n2, axes=AXES)
+    back = spectral.fft2(dev(x), inverse=True, impl=impl)
+    assert_transform_close(back, ref.ifft2(x), n1 * n2, axes=AXES)
+
+
 # Columns of 2048 and 4096 points run as two passes of 64 x (n1 / 64) (tiles of 32 or more
 # columns), for complex 2D and for the column passes of the real column-first transforms.
 LONG_COLUMN_SHAPES = [(2048, 32), (2048, 64), (4096, 32), (4096, 128)]
