@@ -800,21 +800,6 @@ __global__ void __launch_bounds__(F::NT)
 // loads to their first use is straight) measured slower, 37.1 us. So did the same prefetch in
 // the forward transform, which stays one array per workgroup (33.1 against 32.6 us).
 
-// The lane's index within the workgroup, as a value the compiler cannot see through. Taken once
-// per turn of a persistent loop, it keeps the lane's loop-invariant values (twiddle bases,
-// addresses) from being hoisted out of the loop and held in registers across all of it: the
-// loop body then needs about the registers of one array's work (110 VGPRs at 128 x 128 against
-// 152 without), so two workgroups of 512 lanes still fit on a CU (128 VGPRs each). The bound
-// 0 <= tid < NT is restated for the compiler.
-template <int NT>
-__device__ __forceinline__ int opaque_tid()
-{
-    int tid = static_cast<int>(threadIdx.x);
-    asm volatile("" : "+v"(tid));
-    __builtin_assume(tid >= 0 && tid < NT);
-    return tid;
-}
-
 template <class F>
 __global__ void __launch_bounds__(F::NT)
     irfft2_full_persistent_kernel(const cf32* __restrict__ x, cf32* __restrict__ z,

@@ -931,6 +931,75 @@ __global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch
     }
 }
 
+// The lane's index within the workgroup, as a value the compiler cannot see through. Taken once
+// per turn of a persistent loop, it keeps the lane's loop-invariant values (twiddle bases,
+// addresses) from being hoisted out of the loop and held in registers across all of it: the
+// loop body then needs about the registers of one item's work (the single-pass irfft2 at
+// 128 x 128: 110 VGPRs against 152 without), so as many workgroups fit on a CU as without the
+// loop. The bound 0 <= tid < NT is restated for the compiler.
+template <int NT>
+__device__ __forceinline__ int opaque_tid()
+{
+    int tid = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(tid));
+    __builtin_assume(tid >= 0 && tid < NT);
+    return tid;
+}
+
+// Persistent fft_kernel for plans of one transform per workgroup whose I/O policy reads and
+// writes HBM directly (the 16384-point C2C: 1024 lanes, 139 KB of LDS, one per CU). Workgroup
+// g takes transforms g, g + G, ... (G = gridDim.x, the workgroups resident at once). Before a
+// transform's stages it issues the next transform's loads into a second register set, so they
+// are in flight during the stages' exchanges and the stores. Each exchange of run_stages starts
+// with a barrier, so one transform's stages do not write the LDS before the previous
+// transform's last reads.
+template <class P, bool Inv, bool Table, class Io>
+__global__ void __launch_bounds__(P::kThreads)
+    fft_persistent_kernel(Io io, long long batch, const cf32* table)
+{
+    static_assert(P::T == 1 && Io::template direct_in<P>() && Io::template direct_out<P>() &&
+                      !HasInAll<Io>::value,
+                  "one transform per workgroup, loaded and stored directly");
+    __shared__ cf32 lds[P::kStride];
+    constexpr int R0 = P::template radix<0>();
+    constexpr int RL = P::template radix<P::kStages - 1>();
+
+    cf32 v[P::E];
+    const auto fetch = [&](long long t, int lane) __attribute__((always_inline)) {
+#pragma unroll
+        for (int b = 0; b < P::E / R0; ++b) {
+#pragma unroll
+            for (int r = 0; r < R0; ++r) {
+                v[b * R0 + r] = io.template in<P>(t, input_index<P, 0>(lane, b, r));
+            }
+        }
+    };
+
+    long long t = blockIdx.x;
+    fetch(t, threadIdx.x);
+#pragma unroll 1
+    for (; t < batch; t += gridDim.x) {
+        const int lane = opaque_tid<P::kThreads>();
+        cf32 u[P::E];
+#pragma unroll
+        for (int e = 0; e < P::E; ++e) {
+            u[e] = v[e];
+        }
+        const long long next = t + gridDim.x;
+        if (next < batch) {
+            fetch(next, lane);
+        }
+        run_stages<P, 0, Inv, Table>(u, lds, lane, table);
+#pragma unroll
+        for (int b = 0; b < P::E / RL; ++b) {
+#pragma unroll
+            for (int r = 0; r < RL; ++r) {
+                io.template out<P>(t, lane + b * P::L + r * (P::N / RL), u[b * RL + r]);
+            }
+        }
+    }
+}
+
 // --- I/O policies ---------------------------------------------------------------------------
 
 // Contiguous complex rows. Pruned: rows of x hold keep_in values (the rest of each transform is

@@ -173,6 +173,13 @@ void launch_persistent(int threads, long long items, hipStream_t stream, Args...
 #endif
 inline constexpr bool kFusedPersistent = SPX_FUSED_PERSISTENT != 0;
 
+// The single-pass 16384-point C2C runs persistent (fft_persistent_kernel); 0 keeps one transform
+// per workgroup.
+#ifndef SPX_LARGE_PERSISTENT
+#define SPX_LARGE_PERSISTENT 1
+#endif
+inline constexpr bool kPersistentLarge = SPX_LARGE_PERSISTENT != 0;
+
 // Strided columns of 256, 512 and 1024 points, and of 64 and 128 points in wide matrices, run
 // persistent (columns_kernel); other lengths keep one tile per workgroup. The 1024-point tiles hold
 // 8 columns of 16 values per lane, one wave per column (workgroups of 512 lanes), in XCD order:
@@ -235,13 +242,31 @@ void dispatch_strided_columns(int n, const StridedIo& io, long long batch, hipSt
 template <int N, int R>
 using LargePlan = Plan<N, (N == 16384 && R == 8) ? 16 : R, N / kMaxBlock, kMaxBlock>;
 
+// The single-pass large plans. Where one workgroup fills a CU's LDS (16384 points, 139 KB),
+// complex rows run persistent (fft_persistent_kernel): nothing else overlaps that workgroup's
+// load phase. Measured over 2^24 points (four alternated rounds): 16384 66.1 -> 64.2 us, but
+// 8192 (two workgroups per CU) 60.3 -> 63.4 us, so 8192 and the real transforms' combine and
+// prepare keep one transform per workgroup.
+template <class P, bool Inv, bool Table, class Io>
+void launch_large(const Io& io, long long batch, hipStream_t stream)
+{
+    if constexpr (kPersistentLarge && P::N >= 16384 && Io::template direct_in<P>() &&
+                  Io::template direct_out<P>() && !HasInAll<Io>::value && !HasFinal<Io>::value &&
+                  !HasStage0<Io>::value) {
+        launch_persistent<fft_persistent_kernel<P, Inv, Table, Io>>(
+            P::kThreads, batch, stream, io, batch, Table ? twiddle_table() : nullptr);
+    } else {
+        launch<P, Inv, Table>(io, batch, stream);
+    }
+}
+
 template <int R, bool Inv, bool Table, class Io>
 void dispatch_large(int n, const Io& io, long long batch, hipStream_t stream)
 {
     if (n == 8192) {
-        launch<LargePlan<8192, R>, Inv, Table>(io, batch, stream);
+        launch_large<LargePlan<8192, R>, Inv, Table>(io, batch, stream);
     } else if (n == 16384) {
-        launch<LargePlan<16384, R>, Inv, Table>(io, batch, stream);
+        launch_large<LargePlan<16384, R>, Inv, Table>(io, batch, stream);
     } else {
         throw InvalidArgument("stockham: unsupported size " + str(n));
     }

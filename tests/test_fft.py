@@ -76,9 +76,11 @@ def test_c2c_parity_with_a_partly_filled_last_workgroup(rng, impl, n, batch):
 
 @pytest.mark.parametrize("direction", DIRECTIONS)
 @pytest.mark.parametrize("impl", STOCKHAM)
-@pytest.mark.parametrize(("n", "batch"), [(8192, 513), (16384, 300)])
+@pytest.mark.parametrize(("n", "batch"), [(8192, 513), (8192, 1283), (16384, 300), (16384, 600)])
 def test_c2c_parity_with_more_large_transforms_than_cus(rng, n, batch, impl, direction):
-    # Every workgroup of 1024 lanes owns one whole transform, over several rounds of the grid.
+    # Every workgroup of 1024 lanes owns one whole transform. At 16384 points it loops over
+    # transforms g, g + G, ... (G = 256 resident workgroups); the batches take the loop round twice
+    # and three times, the last time for some workgroups only. At 8192 the grid covers the batch.
     x = random_complex(rng, (batch, n))
     assert_transform_close(c2c(x, impl, direction), oracle(x, direction), n)
 
