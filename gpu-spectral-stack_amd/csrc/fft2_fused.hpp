@@ -58,7 +58,7 @@ constexpr int column_values()
 template <int N1, int R>
 constexpr int column_radix()
 {
-    return (R == 8 && column_values<N1, R>() >= 16) ? 16 : R;
+    return (kRadix16 && R == 8 && column_values<N1, R>() >= 16) ? 16 : R;
 }
 
 template <int N1_, int M_, int R, bool Table, int BudgetKB = 80, int Threads = 512>

@@ -348,6 +348,14 @@ struct Plan {
     static constexpr int span_before() { return 1 << (S * clog2(R)); }
 };
 
+// Radix-16 stages where a lane holds 16 values anyway (the 4096-point plan, the single-pass 2D
+// columns, the FIR's 1024-point blocks): one LDS exchange and one twiddle stage fewer than radix
+// 8 at the same lanes and registers. 0 keeps radix 8 there, for A/B builds.
+#ifndef SPX_RADIX16
+#define SPX_RADIX16 1
+#endif
+inline constexpr bool kRadix16 = SPX_RADIX16 != 0;
+
 // Values per lane for an N-point transform with radix-R stages: as few as hold one butterfly (and
 // at least 4: radix-2 plans with E = 2 measured 15-20 % slower), but enough that a transform needs
 // at most 256 lanes. Fewer values per lane means fewer VGPRs and more resident waves, and on

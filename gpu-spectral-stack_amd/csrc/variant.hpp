@@ -63,13 +63,13 @@ void launch(const Io& io, long long batch, hipStream_t stream)
 template <int N, int R>
 constexpr int plan_radix()
 {
-    return (R == 8 && N == 4096) ? 16 : R;
+    return (kRadix16 && R == 8 && N == 4096) ? 16 : R;
 }
 
 template <int N, int R>
 constexpr int plan_e()
 {
-    return (R == 8 && N == 4096) ? 16 : default_e<N, R>();
+    return (kRadix16 && R == 8 && N == 4096) ? 16 : default_e<N, R>();
 }
 
 template <int R, bool Inv, bool Table, class Io>
@@ -1376,7 +1376,8 @@ struct RfDriver {
     // alternated rounds); at 256 and 512 points the same change measured 11 % slower, at 2048
     // no different.
     template <int N>
-    using FirPlanOf = std::conditional_t<(R == 8 && N == 1024), dev::Plan<N, 16, 16>, PlanOf<N>>;
+    using FirPlanOf =
+        std::conditional_t<(dev::kRadix16 && R == 8 && N == 1024), dev::Plan<N, 16, 16>, PlanOf<N>>;
 
     static void check(long long n, int nfft, long long rows, const char* who)
     {
