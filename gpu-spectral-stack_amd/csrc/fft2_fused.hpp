@@ -61,7 +61,16 @@ constexpr int column_radix()
     return (kRadix16 && R == 8 && column_values<N1, R>() >= 16) ? 16 : R;
 }
 
-template <int N1_, int M_, int R, bool Table, int BudgetKB = 80, int Threads = 512>
+// Complex kernels' tile rows hold M values, pad(M - 1) + 1 slots; real ones the M + 1 bins,
+// pad(M) + 1. Sized as complex, a 128 x 128 complex tile takes the padded layout below within
+// 160 KB (rows 136 values apart, 146,880 B); sized as real it needs rows 168 apart, which does
+// not fit, and falls back to odd strides. 0 sizes complex rows as real ones, for A/B builds.
+#ifndef SPX_COMPLEX_TILE_ROWS
+#define SPX_COMPLEX_TILE_ROWS 1
+#endif
+
+template <int N1_, int M_, int R, bool Table, int BudgetKB = 80, int Threads = 512,
+          bool Complex = false>
 struct Fused2d {
     static constexpr int N1 = N1_;                 // rows (column transform length)
     static constexpr int M = M_;                   // complex values per real row (n2 / 2)
@@ -74,14 +83,16 @@ struct Fused2d {
     // radix-8 variants take radix-16 stages (column_radix).
     using PC = Plan<N1, column_radix<N1, R>(), column_values<N1, R>()>;
     // Tile layout: row f, column c of array a at tile[a kTile + row_at(f) + pad(c)]. A tile row
-    // holds pad(M) + 1 values (a padded row transform, or the M + 1 bins). One array per
+    // holds kRowValues values (a padded row transform, or the M + 1 bins). One array per
     // workgroup with rows of 64 complex values or more (128 x 128): row f in tile row pad(f),
     // tile rows TS = 8 mod 32 apart, and the column passes interleave their columns across each
     // wave's lanes (col_slot / col_lane), which keeps each half-wave on distinct banks in all but
     // the first stage's writes (bank conflicts 14 % of column and 20 % of row LDS cycles, against
     // 50-56 % for odd strides with contiguous column groups). Otherwise rows are TS apart, TS odd.
-    static constexpr int kTsOdd = (pad(M) + 1) | 1;
-    static constexpr int kTsPadded = ((pad(M) + 1 + 23) / 32) * 32 + 8;
+    static constexpr int kRowValues =
+        (Complex && SPX_COMPLEX_TILE_ROWS != 0) ? pad(M - 1) + 1 : pad(M) + 1;
+    static constexpr int kTsOdd = kRowValues | 1;
+    static constexpr int kTsPadded = ((kRowValues + 23) / 32) * 32 + 8;
     static constexpr int kRowsPadded = pad(N1 - 1) + 1;
     static constexpr bool kPadRows = N1 * 2 * M >= 16384 && M >= 64 && N1 >= 16
                                      && kRowsPadded * kTsPadded * 8 <= BudgetKB * 1024;

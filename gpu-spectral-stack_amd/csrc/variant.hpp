@@ -1169,13 +1169,13 @@ struct Fused2dDriver {
     template <int N1, int N2>
     static void launch_c2c(const cf32* x, cf32* y, int batch, bool inverse, hipStream_t stream)
     {
-        // M = N2: complex rows of n2 values; 128 x 128 takes a 140 KB tile. With 128 rows, one
+        // M = N2: complex rows of n2 values; 128 x 128 takes a 143 KB tile. With 128 rows, one
         // array per workgroup of 1024 lanes: 128 x 128 76.4 -> 71.7 us and 128 x 64 56.4 ->
         // 53.4 us over 2^24 points on MI355X against 512 lanes (64 x 128 unchanged; the real
         // kernels at 128 x 128 measured 39 % slower with 1024, and still 3-6 % slower with one
         // row pass, 8-value columns and 43-55 VGPRs, i.e. 8 waves per SIMD).
         using F = dev::Fused2d<N1, N2, R, Table, (N1 * N2 > 8192 ? 160 : 80),
-                               (N1 >= 128 ? 1024 : 512)>;
+                               (N1 >= 128 ? 1024 : 512), true>;
         const long long blocks = (static_cast<long long>(batch) + F::AP - 1) / F::AP;
         const cf32* table = Table ? twiddle_table() : nullptr;
         const float scale = inverse ? 1.0f / static_cast<float>(N1 * N2) : 1.0f;
