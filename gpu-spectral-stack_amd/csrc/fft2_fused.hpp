@@ -470,7 +470,7 @@ __global__ void __launch_bounds__(F::NT)
         constexpr int p = decltype(pi)::value;
         const int row = p * F::RPP + tid / PR::L;
         cf32* const s = tile + (row / F::N1) * F::kTile + F::row_at(row % F::N1);
-        run_stages<PR, 0, false, F::kTable>(v[p], s, lane, table);
+        run_stages<PR, 0, false, F::kTable, RowExchange<PR, F::TS>>(v[p], s, lane, table);
         lds_sync<true>();
         final_write<PR>(s, v[p], lane);
         lds_sync<true>();
@@ -650,7 +650,7 @@ __global__ void __launch_bounds__(F::NT)
         lds_sync<true>();
         cf32 v[PR::E];
         stage_read<PR, 0>(s, v, lane);
-        run_stages<PR, 0, true, F::kTable>(v, s, lane, table);
+        run_stages<PR, 0, true, F::kTable, RowExchange<PR, F::TS>>(v, s, lane, table);
         if constexpr (PR::L >= 16) {
             // Rows of 16 lanes or more: every store is a run of at least 128 bytes.
             if (a < count) {
@@ -748,7 +748,7 @@ __global__ void __launch_bounds__(F::NT)
                 }
             }
         }
-        run_stages<PR, 0, Inv, F::kTable>(v, s, lane, table);
+        run_stages<PR, 0, Inv, F::kTable, RowExchange<PR, F::TS>>(v, s, lane, table);
         lds_sync<true>();
         final_write<PR>(s, v, lane);
     }
@@ -867,7 +867,7 @@ __global__ void __launch_bounds__(F::NT)
             lds_sync<true>();
             cf32 u[PR::E];
             stage_read<PR, 0>(s, u, lane);
-            run_stages<PR, 0, true, F::kTable>(u, s, lane, table);
+            run_stages<PR, 0, true, F::kTable, RowExchange<PR, F::TS>>(u, s, lane, table);
             if constexpr (PR::L >= 16) {
                 constexpr int RL = PR::template radix<PR::kStages - 1>();
 #pragma unroll
@@ -945,7 +945,8 @@ __global__ void __launch_bounds__(F::NT)
             static_for<0, kPasses>([&](auto pi) {
                 constexpr int p = decltype(pi)::value;
                 cf32* const s = tile + F::row_at(p * F::RPP + tid / PR::L);
-                run_stages<PR, 0, Inv, F::kTable>(v[p], s, lane, table);
+                run_stages<PR, 0, Inv, F::kTable, RowExchange<PR, F::TS>>(v[p], s, lane,
+                                                                       table);
                 lds_sync<true>();
                 final_write<PR>(s, v[p], lane);
             });

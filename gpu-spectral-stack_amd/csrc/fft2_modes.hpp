@@ -45,7 +45,10 @@ struct Modes2d {
     static constexpr int kScratch = RPP * TR;
     static constexpr int kTile = (kPadRows ? pad(N1 - 1) + 1 : N1) * TC;
     using ColLay = std::conditional_t<kPadRows, PaddedRows<TC>, Strided<TC>>;
-    __host__ __device__ static constexpr int tile_row(int f) { return (kPadRows ? pad(f) : f) * TC; }
+    __host__ __device__ static constexpr int tile_row(int f)
+    {
+        return (kPadRows ? pad(f) : f) * TC;
+    }
     static constexpr int kMaxIo = (N1 * WMax + NT - 1) / NT;  // flat modes per lane, at most
 
     static_assert(kPasses >= 1 && N1 % RPP == 0, "row passes cover the rows exactly");
@@ -98,7 +101,7 @@ __global__ void __launch_bounds__(F::NT)
     const cf32 base = twiddle_of<2 * F::M, false>(lane);
     static_for<0, F::kPasses>([&](auto pi) {
         constexpr int p = decltype(pi)::value;
-        run_stages<PR, 0, false, F::kTable>(v[p], s, lane, table);
+        run_stages<PR, 0, false, F::kTable, RowExchange<PR, F::TR>>(v[p], s, lane, table);
         lds_sync<true>();
         final_write<PR>(s, v[p], lane);
         lds_sync<true>();
@@ -270,7 +273,7 @@ __global__ void __launch_bounds__(F::NT)
             const cf32 od = cmul(d, off == 0 ? base : cmul(base, c));
             v[e] = cf32{ev.re - od.im, ev.im + od.re};
         });
-        run_stages<PR, 0, true, F::kTable>(v, s, lane, table);
+        run_stages<PR, 0, true, F::kTable, RowExchange<PR, F::TR>>(v, s, lane, table);
         if constexpr (PR::L >= 16) {
             // Rows of 16 lanes or more: every store is a run of at least 128 bytes.
             cf32* const dst = out + row * F::M;

@@ -405,8 +405,9 @@ __device__ __forceinline__ void lds_sync()
 
 // --- stage pieces ---------------------------------------------------------------------------
 //
-// A transform's values sit in LDS in one of two layouts: element i at s[Lay::at(i)].
+// A transform's values sit in LDS in one of these layouts: element i at s[Lay::at(i)].
 //   Padded         one complex of padding after every 16 (a transform stored as a row)
+//   Padded8        one after every 8 (the 64-point rows' exchange, see RowExchange)
 //   Strided<ST>    every ST values (a column of a row-major tile whose rows are ST long)
 //   PaddedRows<ST> a column of a tile with a spare row after every 16 rows
 // LDS addresses are a per-lane base plus a compile-time offset. For Strided that is linearity;
@@ -418,6 +419,25 @@ __device__ __forceinline__ void lds_sync()
 struct Padded {
     __host__ __device__ static constexpr int at(int i) { return pad(i); }
 };
+
+struct Padded8 {
+    __host__ __device__ static constexpr int at(int i) { return i + (i >> 3); }
+};
+
+// The layout of a row transform's stage exchanges when four rows of a half-wave sit RowStride
+// values apart. The 64-point plan (8 lanes of 8, two radix-8 stages) with rows 8 mod 32 apart
+// exchanges free of bank conflicts in Padded8 (64 banks of 4 bytes, 8-byte accesses served a
+// half-wave at a time): the first stage's writes, lane l at 8 l + r, fill all 32 eight-byte
+// slots of the four rows, where Padded leaves them 2-way conflicted at every row stride. It
+// needs 71 slots per row (Padded: 67). SPX_ROW_EXCHANGE_PAD8=0 keeps Padded, for A/B builds.
+#ifndef SPX_ROW_EXCHANGE_PAD8
+#define SPX_ROW_EXCHANGE_PAD8 1
+#endif
+template <class P, int RowStride>
+using RowExchange =
+    std::conditional_t<(SPX_ROW_EXCHANGE_PAD8 != 0 && P::N == 64 && P::L == 8 &&
+                        RowStride % 32 == 8 && RowStride >= 71),
+                       Padded8, Padded>;
 
 template <int Stride>
 struct Strided {
@@ -825,10 +845,10 @@ struct HasInAll<Io, std::void_t<decltype(Io::kInAll)>> : std::bool_constant<Io::
 // Workgroup order across the XCDs. The dispatcher hands workgroup b to XCD b mod 8, and each XCD
 // has its own L2, so in plain order the neighbouring tiles of a strided pass (whose rows share
 // cache lines and DRAM pages) run on different XCDs. An I/O policy with
-// `static constexpr int kXcdChunk = C` renumbers each span of 8 C workgroups so that every XCD takes
-// C consecutive tiles of the span; a trailing partial span keeps its order. Spans stay short: the
-// XCDs then work on neighbouring regions, where XCDs working on regions far apart (C = grid / 8)
-// measured slower than plain order.
+// `static constexpr int kXcdChunk = C` renumbers each span of 8 C workgroups so that every XCD
+// takes C consecutive tiles of the span; a trailing partial span keeps its order. Spans stay
+// short: the XCDs then work on neighbouring regions, where XCDs working on regions far apart
+// (C = grid / 8) measured slower than plain order.
 template <class Io, class = void>
 struct XcdChunk : std::integral_constant<int, 0> {};
 template <class Io>
