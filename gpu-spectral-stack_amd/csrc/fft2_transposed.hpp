@@ -59,35 +59,64 @@ __device__ __forceinline__ void store_transposed(const cf32* lds, cf32* y, long 
     }
 }
 
-// Element k < len of each staged transform read from the transposed side into LDS (every load
-// issued before the first LDS write).
-template <class P, class G>
-__device__ __forceinline__ void load_transposed(cf32* lds, const cf32* x, long long first,
-                                                int count, int tid, int rows, int len,
-                                                bool stream_in)
+// A lane's values of one transposed load: element tid / T + s L of its transform, s < steps,
+// for transforms of len = N + Plus values (Plus 0 or 1).
+template <class P, int Plus>
+constexpr int transposed_steps()
 {
-    static_assert(G::kT == P::T && G::kThreads == P::kThreads, "the whole workgroup loads");
-    const int j = tid % P::T;
-    if (!G::kFull && j >= count) {
+    return (P::N + Plus + P::L - 1) / P::L;
+}
+
+// The transposed side's element k < len of each of the count staged transforms into registers
+// (lanes of transforms past count load nothing).
+template <class P, int Plus>
+__device__ __forceinline__ void fetch_transposed(
+    cf32 (&val)[(transposed_steps<P, Plus>())], const cf32* x, long long first, int count,
+    int tid, int rows, bool stream_in)
+{
+    constexpr int len = P::N + Plus;
+    if (tid % P::T >= count) {
         return;
     }
     const cf32* const base = x + transposed_origin<P>(first, tid, rows, len);
-    constexpr int kSteps = (P::N + 1 + P::L - 1) / P::L;
-    cf32 val[kSteps];
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
+    for (int s = 0; s < transposed_steps<P, Plus>(); ++s) {
         const int k = tid / P::T + s * P::L;
         const bool in = (s + 1) * P::L <= P::N || k < len;
         const cf32* const src = base + static_cast<long long>(in ? k : 0) * rows;
         val[s] = in ? (stream_in ? ld_stream(src) : *src) : czero();
     }
+}
+
+// The fetched values into their transforms' LDS rows.
+template <class P, int Plus>
+__device__ __forceinline__ void park_transposed(
+    cf32* lds, const cf32 (&val)[(transposed_steps<P, Plus>())], int count, int tid)
+{
+    constexpr int len = P::N + Plus;
+    const int j = tid % P::T;
+    if (j >= count) {
+        return;
+    }
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
+    for (int s = 0; s < transposed_steps<P, Plus>(); ++s) {
         const int k = tid / P::T + s * P::L;
         if ((s + 1) * P::L <= P::N || k < len) {
             lds[j * P::kStride + pad(k)] = val[s];
         }
     }
+}
+
+// Element k < len of each staged transform read from the transposed side into LDS (every load
+// issued before the first LDS write).
+template <class P, class G, int Plus>
+__device__ __forceinline__ void load_transposed(cf32* lds, const cf32* x, long long first,
+                                                int count, int tid, int rows, bool stream_in)
+{
+    static_assert(G::kT == P::T && G::kThreads == P::kThreads, "the whole workgroup loads");
+    cf32 val[transposed_steps<P, Plus>()];
+    fetch_transposed<P, Plus>(val, x, first, G::kFull ? P::T : count, tid, rows, stream_in);
+    park_transposed<P, Plus>(lds, val, G::kFull ? P::T : count, tid);
 }
 
 // Contiguous rows of N complex values into LDS, as the group's staged load.
@@ -249,7 +278,25 @@ struct TransposedToRowsIoT {
     template <class P, class G>
     __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
     {
-        load_transposed<P, G>(lds, x, first, count, tid, rows, P::N, stream_in);
+        load_transposed<P, G, 0>(lds, x, first, count, tid, rows, stream_in);
+    }
+
+    // The load in two halves, for the persistent tile loop (tiles_persistent_kernel).
+    static constexpr bool kFetch = true;
+    template <class P>
+    static constexpr int fetch_steps() { return transposed_steps<P, 0>(); }
+    template <class P>
+    __device__ __forceinline__ void fetch(cf32 (&val)[(transposed_steps<P, 0>())],
+                                          long long first, int count, int tid) const
+    {
+        fetch_transposed<P, 0>(val, x, first, count, tid, rows, stream_in);
+    }
+    template <class P>
+    __device__ __forceinline__ void park(cf32* lds,
+                                         const cf32 (&val)[(transposed_steps<P, 0>())],
+                                         int count, int tid) const
+    {
+        park_transposed<P, 0>(lds, val, count, tid);
     }
 
     template <class P, class G>
@@ -267,6 +314,72 @@ struct TransposedToRowsIoT {
 };
 
 using TransposedToRowsIo = TransposedToRowsIoT<0>;
+
+// Persistent form of fft_kernel for the transposed-side loads: workgroup g takes tiles of T
+// transforms g', g' + G, ... (g' = g in the policy's XCD order, G = gridDim.x) and issues the
+// next tile's loads into registers once the current tile is in LDS, so they are in flight during
+// its stages and stores (the pattern of columns_kernel).
+template <class P, bool Inv, bool Table, class Io>
+__global__ void __launch_bounds__(P::kThreads) __attribute__((amdgpu_waves_per_eu(8)))
+    tiles_persistent_kernel(Io io, long long batch, const cf32* table)
+{
+    static_assert(Io::kGroupIsBlock && Io::kFetch && !Io::template direct_in<P>(),
+                  "loads staged by the whole workgroup, in two halves");
+    __shared__ cf32 lds[P::T * P::kStride];
+    using Full = Group<P::T, P::kThreads, true>;
+    using Tail = Group<P::T, P::kThreads, false>;
+    const long long tiles = (batch + P::T - 1) / P::T;
+    const auto count_of = [batch](long long tile) {
+        const long long left = batch - tile * P::T;
+        return left >= P::T ? P::T : static_cast<int>(left);
+    };
+    cf32 val[Io::template fetch_steps<P>()];
+    const long long offset = xcd_order<XcdChunk<Io>::value>(blockIdx.x, gridDim.x);
+    if (offset < tiles) {
+        io.template fetch<P>(val, offset * P::T, count_of(offset), threadIdx.x);
+    }
+#pragma unroll 1
+    for (long long tile = offset; tile < tiles; tile += gridDim.x) {
+        const int tid = opaque_tid<P::kThreads>();
+        const int lane = tid % P::L;
+        const int u = tid / P::L;
+        cf32* const s = lds + u * P::kStride;
+        const int count = count_of(tile);
+        io.template park<P>(lds, val, count, tid);
+        lds_sync<false>();
+        const long long next = tile + gridDim.x;
+        if (next < tiles) {
+            io.template fetch<P>(val, next * P::T, count_of(next), tid);
+        }
+        // Transforms past the batch run the stages on what the tile holds but store nothing.
+        cf32 v[P::E];
+        stage_read<P, 0>(s, v, lane);
+        run_stages<P, 0, Inv, Table>(v, s, lane, table);
+        if constexpr (Io::template direct_out<P>()) {
+            if (u < count) {
+                constexpr int RL = P::template radix<P::kStages - 1>();
+                const long long t = tile * P::T + u;
+#pragma unroll
+                for (int b = 0; b < P::E / RL; ++b) {
+#pragma unroll
+                    for (int r = 0; r < RL; ++r) {
+                        io.template out<P>(t, lane + b * P::L + r * (P::N / RL), v[b * RL + r]);
+                    }
+                }
+            }
+        } else {
+            lds_sync<P::kWaveLocal>();
+            final_write<P>(s, v, lane);
+            lds_sync<false>();
+            if (count == P::T) {
+                io.template store<P, Full>(lds, tile * P::T, P::T, tid);
+            } else {
+                io.template store<P, Tail>(lds, tile * P::T, count, tid);
+            }
+        }
+        lds_sync<false>();  // the tile is read before the next one lands
+    }
+}
 
 struct C2rTransposedToRowsIo {
     static constexpr bool kGroupIsBlock = true;
@@ -292,7 +405,7 @@ struct C2rTransposedToRowsIo {
     __device__ __forceinline__ void load(cf32* lds, long long first, int count, int tid) const
     {
         static_assert(pad(P::N) < P::kStride, "X[m] fits the row's LDS stride");
-        load_transposed<P, G>(lds, x, first, count, tid, rows, P::N + 1, false);
+        load_transposed<P, G, 1>(lds, x, first, count, tid, rows, false);
         lds_sync<false>();
         prepare_pairs<P, G>(lds, count, tid, scale);
     }

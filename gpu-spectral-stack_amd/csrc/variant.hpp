@@ -99,14 +99,19 @@ void dispatch(int n, const Io& io, long long batch, hipStream_t stream)
 }
 
 // Strided columns: the plans of column_e / column_threads.
+// The column plans' launch: persistent (tiles_persistent_kernel) for I/O policies whose load
+// splits into a register fetch and an LDS park, else fft_kernel. Defined below.
+template <class P, bool Inv, bool Table, class Io>
+void launch_tiles(const Io& io, long long batch, hipStream_t stream);
+
 template <int R, bool Inv, bool Table, class Io>
 void dispatch_columns(int n, const Io& io, long long batch, hipStream_t stream)
 {
     switch (n) {
 #define SPX_CASE(N)                                                                          \
     case N:                                                                                  \
-        launch<Plan<N, R, column_e<N, R>(), column_threads<N, R>()>, Inv, Table>(io, batch,   \
-                                                                               stream);      \
+        launch_tiles<Plan<N, R, column_e<N, R>(), column_threads<N, R>()>, Inv, Table>(       \
+            io, batch, stream);                                                              \
         break;
         SPX_CASE(2)
         SPX_CASE(4)
@@ -241,6 +246,33 @@ void dispatch_strided_columns(int n, const StridedIo& io, long long batch, hipSt
 // 16384 at 50 % (radix 8) and 53 % (radix 16), where the four-step split took 8 % and 13 %.
 template <int N, int R>
 using LargePlan = Plan<N, (N == 16384 && R == 8) ? 16 : R, N / kMaxBlock, kMaxBlock>;
+
+template <class Io, class = void>
+struct HasFetch : std::false_type {};
+template <class Io>
+struct HasFetch<Io, std::void_t<decltype(Io::kFetch)>> : std::bool_constant<Io::kFetch> {};
+
+// The transposed-side passes of the transpose column method run persistent where their policy
+// has fetch / park, at 512 points: 16-transform tiles of 1024 lanes, two per CU. irfft2 512² x 64
+// by that method went from 59.7 to 53.6 us (four alternated rounds). At 64-256 points (tiles of
+// 256 or 512 lanes, more per CU) and at 1024 (8-transform tiles) the loop measured 3-4 % slower,
+// so those keep one tile per workgroup. SPX_TILES_PERSISTENT=0: one tile per workgroup at every
+// size, for A/B builds.
+#ifndef SPX_TILES_PERSISTENT
+#define SPX_TILES_PERSISTENT 1
+#endif
+
+template <class P, bool Inv, bool Table, class Io>
+void launch_tiles(const Io& io, long long batch, hipStream_t stream)
+{
+    if constexpr (SPX_TILES_PERSISTENT != 0 && HasFetch<Io>::value && P::N == 512) {
+        launch_persistent<tiles_persistent_kernel<P, Inv, Table, Io>>(
+            P::kThreads, (batch + P::T - 1) / P::T, stream, io, batch,
+            Table ? twiddle_table() : nullptr);
+    } else {
+        launch<P, Inv, Table>(io, batch, stream);
+    }
+}
 
 // The single-pass large plans. Where one workgroup fills a CU's LDS (16384 points, 139 KB),
 // complex rows run persistent (fft_persistent_kernel): nothing else overlaps that workgroup's
