@@ -94,11 +94,10 @@ __device__ __forceinline__ cf32 expi_pi(float a)
 
 // --- streaming global accesses ---------------------------------------------------------------
 //
-// Every HBM byte of a transform is read once and written once. Stores always carry the
+// Every HBM byte of a transform is read once and written once. Stores of final outputs carry the
 // nontemporal hint (they stream through the caches instead of displacing other lines), and so do
-// the loads of complex-to-complex transforms; the loads of the real transforms are plain, which
-// measured faster for them on MI355X (C2C: +4-6 % of peak with both hints; R2C / C2R: +8-12 %
-// with nontemporal stores, but 5-10 % slower again with nontemporal loads).
+// the loads of complex-to-complex transforms (+4-6 % of peak with both hints on MI355X). The
+// real transforms' loads take the hint where it measured faster (R2cIoT, C2rIo).
 
 using f2v = float __attribute__((ext_vector_type(2)));
 
@@ -111,6 +110,15 @@ __device__ __forceinline__ cf32 ld_stream(const cf32* p)
 __device__ __forceinline__ void st_stream(cf32* p, cf32 a)
 {
     __builtin_nontemporal_store(f2v{a.re, a.im}, reinterpret_cast<f2v*>(p));
+}
+
+// A load sent straight to LDS (global_load_lds_dwordx4, nontemporal): each lane of the wave reads
+// 16 bytes at `src`, and lane k's bytes land at lds_base + 16 k. lds_base must be the same for
+// every lane of the wave (the instruction takes it from M0) and 16-byte aligned.
+__device__ __forceinline__ void ld_lds16(const cf32* src, cf32* lds_base)
+{
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                     (__attribute__((address_space(3))) void*)lds_base, 16, 0, 2);
 }
 
 // --- R-point DFTs in registers, X[q] = sum_p v[p] exp(sign 2 pi i p q / R) ---------------------
@@ -842,6 +850,15 @@ struct HasInAll : std::false_type {};
 template <class Io>
 struct HasInAll<Io, std::void_t<decltype(Io::kInAll)>> : std::bool_constant<Io::kInAll> {};
 
+// A policy with `template <class P> static constexpr bool lds_dma_in()` true for plan P sends the
+// workgroup's stage-0 inputs straight to LDS (lds_dma<P>(lds, first, batch, tid): transform u of
+// the workgroup's T at lds + u N, densely), and each lane reads its stage-0 values from there.
+template <class Io, class P, class = void>
+struct HasLdsDmaIn : std::false_type {};
+template <class Io, class P>
+struct HasLdsDmaIn<Io, P, std::void_t<decltype(Io::template lds_dma_in<P>())>>
+    : std::bool_constant<Io::template lds_dma_in<P>()> {};
+
 // Workgroup order across the XCDs. The dispatcher hands workgroup b to XCD b mod 8, and each XCD
 // has its own L2, so in plain order the neighbouring tiles of a strided pass (whose rows share
 // cache lines and DRAM pages) run on different XCDs. An I/O policy with
@@ -896,7 +913,20 @@ __global__ void __launch_bounds__(P::kThreads) fft_kernel(Io io, long long batch
     cf32* const s = lds + u * P::kStride;
 
     cf32 v[P::E];
-    if constexpr (Io::template direct_in<P>()) {
+    if constexpr (HasLdsDmaIn<Io, P>::value) {
+        static_assert(!P::kWaveLocal, "the first exchange's workgroup barrier orders these reads");
+        io.template lds_dma<P>(lds, block * P::T, batch, tid);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed in LDS
+        __syncthreads();                // and every other wave's
+        const cf32* const d = lds + u * P::N;
+#pragma unroll
+        for (int b = 0; b < P::E / P::template radix<0>(); ++b) {
+#pragma unroll
+            for (int r = 0; r < P::template radix<0>(); ++r) {
+                v[b * P::template radix<0>() + r] = d[input_index<P, 0>(lane, b, r)];
+            }
+        }
+    } else if constexpr (Io::template direct_in<P>()) {
         if (t < batch) {
             if constexpr (HasInAll<Io>::value) {
                 io.template in_all<P>(t, lane, v);
@@ -1033,6 +1063,9 @@ __global__ void __launch_bounds__(P::kThreads)
 // Contiguous complex rows. Pruned: rows of x hold keep_in values (the rest of each transform is
 // zero), rows of y keep_out values. PlainOut: plain stores, for an intermediate that the next
 // pass reads (nontemporal otherwise).
+#ifndef SPX_C2C_LDS_DMA
+#define SPX_C2C_LDS_DMA 0
+#endif
 template <bool Pruned, bool PlainOut = false>
 struct C2cIo {
     static constexpr bool kGroupIsBlock = false;
@@ -1043,9 +1076,36 @@ struct C2cIo {
     int keep_out;
 
     template <class P>
-    static constexpr bool direct_in() { return P::L >= 16; }
+    static constexpr bool direct_in() { return P::L >= 16 && !lds_dma_in<P>(); }
     template <class P>
     static constexpr bool direct_out() { return P::L >= 16; }
+
+    // Whole transforms of more than one wave: their stage-0 inputs may go straight to LDS
+    // (SPX_C2C_LDS_DMA), in 16-byte pieces that never straddle two transforms.
+    template <class P>
+    static constexpr bool lds_dma_in()
+    {
+        return SPX_C2C_LDS_DMA != 0 && !Pruned && !P::kWaveLocal && P::N <= 4096 &&
+               (P::T * P::N) % (2 * P::kThreads) == 0 && P::N % 128 == 0;
+    }
+
+    // The workgroup's transforms first .. first + T - 1 (those below batch) to lds densely: each
+    // wave instruction moves 1 KB, 128 values of one transform.
+    template <class P>
+    __device__ __forceinline__ void lds_dma(cf32* lds, long long first, long long batch,
+                                            int tid) const
+    {
+        constexpr int kChunk = 2 * P::kThreads;  // values per workgroup instruction
+        const int wave = tid / 64;
+        const cf32* const src = x + first * P::N;
+#pragma unroll
+        for (int j = 0; j < P::T * P::N / kChunk; ++j) {
+            const int e = j * kChunk + wave * 128;  // the wave's first value
+            if (first + e / P::N < batch) {
+                ld_lds16(src + e + 2 * (tid % 64), lds + e);
+            }
+        }
+    }
 
     template <class P>
     __device__ __forceinline__ cf32 in(long long t, int i) const

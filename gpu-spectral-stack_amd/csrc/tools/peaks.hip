@@ -108,6 +108,37 @@ __global__ void __launch_bounds__(Th) rows_copy_kernel(const f2v* __restrict__ i
     }
 }
 
+// The same rows with the loads sent straight to LDS (global_load_lds_dwordx4, nontemporal): lane
+// k of a wave instruction reads 16 bytes, which land at the wave's LDS base + 16 k. Each wave then
+// reads back only what it loaded and stores it as rows_copy_kernel<Th, 8, true> does, 8 bytes per
+// lane. Workgroup b moves values b Th 8 .. (b + 1) Th 8 - 1.
+template <int Th>
+__global__ void __launch_bounds__(Th) rows_lds_dma_kernel(const f2v* __restrict__ in,
+                                                        f2v* __restrict__ out)
+{
+    constexpr int kSteps = 4;           // 16-byte loads per lane
+    constexpr int kStep = Th * 2;       // values per workgroup step
+    __shared__ f2v lds[kSteps * kStep];  // 16 KB at Th = 256
+    const std::size_t base = static_cast<std::size_t>(blockIdx.x) * kSteps * kStep;
+    const int wave = threadIdx.x / 64;
+    const int l = threadIdx.x % 64;
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+        const int e = k * kStep + wave * 128;  // the wave's 128 values of this step
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(in + base + e + 2 * l),
+                                         (__attribute__((address_space(3))) void*)(lds + e), 16,
+                                         0, 2);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+        const int e = k * kStep + wave * 128;
+        store8<true>(out + base + e + l, lds[e + l]);
+        store8<true>(out + base + e + 64 + l, lds[e + 64 + l]);
+    }
+}
+
 // Uneven mixes: workgroup b reads Th * V contiguous values as rows_copy_kernel does and writes
 // Th of them (each lane the sum of its V), or the mirror (Expand: reads Th, writes each V times).
 // V = 16 is the byte mix of a pruned 2D transform keeping a sixteenth of its input (C4), V = 2
@@ -302,6 +333,13 @@ void launch_rows_tiles(std::size_t values, const f2v* in, f2v* out, hipStream_t 
                        dim3(Th), 0, s, in, out);
 }
 
+template <int Th>
+void launch_rows_lds_dma(std::size_t values, const f2v* in, f2v* out, hipStream_t s)
+{
+    hipLaunchKernelGGL((rows_lds_dma_kernel<Th>), dim3(static_cast<unsigned>(values / (Th * 8))),
+                       dim3(Th), 0, s, in, out);
+}
+
 template <int Th, int V, bool Expand>
 void launch_mix(std::size_t wide_values, const f2v* in, f2v* out, hipStream_t s)
 {
@@ -324,6 +362,8 @@ int run_patterns()
     std::vector<Pattern> ps = {
         {"rows 16 KB chunks, nontemporal", "C1 C2C n = 1024 (2^24 points)", k2e24,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, true>(k2e24, i, o, s); }, {}},
+        {"rows 16 KB chunks, loads straight to LDS, nontemporal", "C1's size, global_load_lds_dwordx4", k2e24,
+         [](const f2v* i, f2v* o, hipStream_t s) { launch_rows_lds_dma<256>(k2e24, i, o, s); }, {}},
         {"rows 16 KB chunks, plain", "2^24 points, plain accesses", k2e24,
          [](const f2v* i, f2v* o, hipStream_t s) { launch_rows<256, 8, false>(k2e24, i, o, s); }, {}},
         {"rows 16 KB chunks, nontemporal", "one pass of C3 512^2 x 64 (2^23 values)", k2e23,
