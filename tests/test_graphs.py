@@ -81,6 +81,26 @@ def test_rfft2_and_irfft2_under_capture(rng, n, arrays):
         inputs)
 
 
+@pytest.mark.parametrize(("shape", "arrays"), [((128, 128), 12), ((64, 128), 6)])
+def test_persistent_complex_fft2_under_capture(rng, shape, arrays):
+    # Persistent kernels: each workgroup loops over arrays g, g + G, ... with G the workgroups
+    # that fit at once (an occupancy query made on the eager warm-up and cached per kernel).
+    inputs = [cuda(random_complex(rng, (arrays, *shape))) for _ in range(3)]
+    replay_matches_eager(
+        lambda x: spectral.fft2(spectral.fft2(x, impl="stockham_r8"), inverse=True,
+                                impl="stockham_r8"),
+        inputs)
+
+
+def test_transpose_method_512_under_capture(rng):
+    # The inverse's transposed-side pass at 512 points is a persistent tile loop.
+    inputs = [cuda(random_real(rng, (2, 512, 512))) for _ in range(3)]
+    replay_matches_eager(
+        lambda x: spectral.irfft2(spectral.rfft2(x, impl="stockham_r8", columns="transpose"),
+                                  512, impl="stockham_r8", columns="transpose"),
+        inputs)
+
+
 def test_fno_modes_under_capture(rng):
     inputs = [cuda(random_real(rng, (2, 8, 128, 128))) for _ in range(3)]
     replay_matches_eager(
