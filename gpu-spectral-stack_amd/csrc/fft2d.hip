@@ -16,9 +16,10 @@
 //                     transposed, then the columns as rows of the workspace, stored transposed
 //                     back; the transposes ride on the passes' LDS tiles (fft2_transposed.hpp),
 //                     two HBM round trips instead of the reference's four (fft2d.cu:138-187)
-//   Transposes        the "transpose" method otherwise (naive, and arrays with a side of 1, or
-//                     real rows of 2): rows, a transpose, the columns as contiguous rows, a
-//                     transpose back (remap.hip's tiled kernel)
+//   Transposes        the "transpose" method otherwise (naive, arrays with a side of 1, real
+//                     rows of 2, and complex arrays with a side beyond 1024): rows, a
+//                     transpose, the columns as contiguous rows, a transpose back (remap.hip's
+//                     tiled kernel)
 //
 // The inverse's 1 / (n1 n2) comes from the 1D passes: 1/n2 in the rows, 1/n1 in the columns.
 
@@ -26,6 +27,16 @@
 
 #include <algorithm>
 #include <climits>
+
+// The complex transform's two transposing passes stage T = 8192 / N transforms per workgroup
+// beyond 512 points, so at 2048 and 4096 points their transposed side moves runs of only 32 and
+// 16 bytes. There the four-kernel route (whole 64 x 64 transpose tiles) measured faster: fft2_c2c
+// 2048^2 282.7 -> 180.8 us and 4096^2 471.5 -> 192.9 us over 2^24 points (three alternated
+// rounds on MI355X). The real transforms keep the two passes at every size (rfft2 2048^2: 74.4
+// against 101.1 us). A larger value here keeps the complex transform's two passes beyond 1024.
+#ifndef SPX_TRANSPOSED_PASSES_MAX_C2C
+#define SPX_TRANSPOSED_PASSES_MAX_C2C 1024
+#endif
 
 namespace spx {
 namespace {
@@ -91,7 +102,8 @@ Plan2d plan_2d(const FftImpl& impl, Columns columns, Kind kind, int n1, int n2, 
         kind != Kind::C2c && impl.real_needs_work ? values(n1, n2 / 2, batch) : 0;
     const Fused2dFns* f = impl.fused;
     if (columns == Columns::Transpose) {
-        if (f != nullptr && n1 >= 2 && n2 >= (kind == Kind::C2c ? 2 : 4)) {
+        if (f != nullptr && n1 >= 2 && n2 >= (kind == Kind::C2c ? 2 : 4) &&
+            (kind != Kind::C2c || std::max(n1, n2) <= SPX_TRANSPOSED_PASSES_MAX_C2C)) {
             p.route = Route::TransposedPasses;
             p.regions = 1;
             p.region = values(n1, w, batch);

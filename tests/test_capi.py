@@ -132,7 +132,8 @@ def test_workspace_queries(lib):
     assert count.value == 0
     # The transpose method: the Stockham implementations' two passes go through one array-sized
     # region (n2 x n1, or (n2/2 + 1) x n1 for real transforms); naive's four kernels through two,
-    # plus its real-row scratch; a side of 1 or real rows of 2 take the four-kernel route too.
+    # plus its real-row scratch; a side of 1, real rows of 2 and complex arrays with a side
+    # beyond 1024 take the four-kernel route too.
     assert lib.spx_fft2_c2c_workspace(3, 0, 8, 8, 2, ctypes.byref(count)) == SPX_OK
     assert count.value == 8 * 8 * 2
     assert lib.spx_fft2_r2c_workspace(3, 0, 8, 8, 2, ctypes.byref(count)) == SPX_OK
@@ -145,6 +146,12 @@ def test_workspace_queries(lib):
     assert count.value == 2 * 8 * 2 * 2
     assert lib.spx_fft2_r2c_workspace(0, 0, 8, 8, 2, ctypes.byref(count)) == SPX_OK
     assert count.value == 2 * 8 * 5 * 2 + 8 * 4 * 2
+    assert lib.spx_fft2_c2c_workspace(3, 0, 1024, 16, 1, ctypes.byref(count)) == SPX_OK
+    assert count.value == 1024 * 16
+    assert lib.spx_fft2_c2c_workspace(3, 0, 2048, 16, 1, ctypes.byref(count)) == SPX_OK
+    assert count.value == 2 * 2048 * 16
+    assert lib.spx_fft2_r2c_workspace(3, 0, 2048, 2048, 1, ctypes.byref(count)) == SPX_OK
+    assert count.value == 2048 * 1025
     # 128 x 128 runs as one single-pass kernel (no workspace); 512 x 512 as rows then columns,
     # through n1 x m2 values per array.
     assert lib.spx_rfft2_modes_workspace(3, 128, 128, 16, 16, 4, ctypes.byref(count)) == SPX_OK
