@@ -11,6 +11,7 @@ import pytest
 import torch
 
 import spectral
+from spectral import rf
 from oracle import reference as ref
 from oracle.tolerance import (
     assert_transform_close,
@@ -178,9 +179,67 @@ def test_random_case_matches_the_oracle(rng, case):
         assert_transform_close(y, expected, n1 * n2, axes=(-2, -1))
 
 
+# --- the radio callers: rf.spectrum and rf.fir --------------------------------------------
+
+def _draw_radio_cases() -> list[tuple]:
+    draw = np.random.default_rng(20261203)
+    one_launch = [b for b in rf.FFT_BACKENDS if b.startswith("stockham")]
+    cases = []
+    for _ in range(CASES_PER_OP // 2):
+        nfft = _pow2(draw, 1, 14)
+        rows = int(draw.integers(1, 4))
+        n = int(draw.integers(0, (1 << 18) // rows + 1))
+        window = ["rect", "hann", "hamming", "blackman"][int(draw.integers(4))]
+        cases.append(("spectrum", one_launch[int(draw.integers(len(one_launch)))], rows, n,
+                      nfft, window))
+    for _ in range(CASES_PER_OP // 2):
+        taps = int(draw.integers(1, 5001))
+        rows = int(draw.integers(1, 4))
+        n = int(draw.integers(1, (1 << 16) // rows + 1))
+        low = max(1, (taps - 1).bit_length())  # the smallest block that holds the filter
+        nfft = None if draw.random() < 0.5 else _pow2(draw, low, max(low, 14))
+        complex_taps = bool(draw.integers(2))
+        cases.append(("fir", one_launch[int(draw.integers(len(one_launch)))], rows, n,
+                      (taps, nfft, complex_taps), ""))
+    return cases
+
+
+RADIO_CASES = _draw_radio_cases()
+
+
+def _radio_id(case) -> str:
+    kind, impl, rows, n, shape, window = case
+    if kind == "spectrum":
+        return f"spectrum-{impl}-{rows}x{n}-nfft{shape}-{window}"
+    taps, nfft, complex_taps = shape
+    return (f"fir-{impl}-{rows}x{n}-taps{taps}{'c' if complex_taps else ''}"
+            f"-nfft{nfft if nfft else 'default'}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", RADIO_CASES, ids=[_radio_id(c) for c in RADIO_CASES])
+def test_random_radio_case_matches_the_oracle(rng, case):
+    from test_rf import filtered, framed_spectrum, rel_l2
+
+    kind, impl, rows, n, shape, window = case
+    x = random_complex(rng, (rows, n))
+    if kind == "spectrum":
+        nfft = shape
+        y = rf.spectrum(dev(x), nfft, window_name=window, fft_impl=impl)
+        assert rel_l2(y, framed_spectrum(x, nfft, window)) < 1e-5 * max(1.0, np.log2(nfft) / 8)
+    else:
+        taps_count, nfft, complex_taps = shape
+        taps = (random_complex(rng, taps_count) if complex_taps
+                else random_real(rng, taps_count))
+        y = rf.fir(dev(x), dev(taps), nfft=nfft, fft_impl=impl)
+        assert tuple(y.shape) == (rows, n)
+        assert rel_l2(y, filtered(x, taps)) < 2e-5
+
+
 def test_the_sample_covers_every_operator_and_implementation():
     ops = {c[0] for c in CASES}
     impls = {c[1] for c in CASES}
     assert ops == {"c2c", "real", "pruned1d", "fft2", "real2", "modes2d"}
     assert set(STOCKHAM) <= impls and "naive" in impls
     assert all(c[2] in ("strided", "transpose", "auto") for c in CASES if c[0] in ("fft2", "real2"))
+    assert {c[0] for c in RADIO_CASES} == {"spectrum", "fir"}
