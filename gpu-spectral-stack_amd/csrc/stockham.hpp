@@ -1060,12 +1060,16 @@ __global__ void __launch_bounds__(P::kThreads)
 
 // --- I/O policies ---------------------------------------------------------------------------
 
-// Contiguous complex rows. Pruned: rows of x hold keep_in values (the rest of each transform is
-// zero), rows of y keep_out values. PlainOut: plain stores, for an intermediate that the next
-// pass reads (nontemporal otherwise).
+// 1 sends the stage-0 loads of the C2C plans of more than one wave straight to LDS, for A/B
+// builds. Off: over 2^24 points those plans ran 0.8-2.9 % slower that way than with register
+// loads, and a copy of C1's rows streamed 6.12 against 6.29 TB/s.
 #ifndef SPX_C2C_LDS_DMA
 #define SPX_C2C_LDS_DMA 0
 #endif
+
+// Contiguous complex rows. Pruned: rows of x hold keep_in values (the rest of each transform is
+// zero), rows of y keep_out values. PlainOut: plain stores, for an intermediate that the next
+// pass reads (nontemporal otherwise).
 template <bool Pruned, bool PlainOut = false>
 struct C2cIo {
     static constexpr bool kGroupIsBlock = false;
