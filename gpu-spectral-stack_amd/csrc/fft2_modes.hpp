@@ -63,6 +63,31 @@ struct Modes2d {
     }
 };
 
+// After a plan's last stage, lane l holds element l + q L of its transform (q < E) in register
+// slot out_slot<P>(q).
+template <class P>
+constexpr int out_slot(int q)
+{
+    constexpr int RL = P::template radix<P::kStages - 1>();
+    for (int e = 0; e < P::E; ++e) {
+        if ((e / RL) * P::L + (e % RL) * (P::N / RL) == q * P::L) {
+            return e;
+        }
+    }
+    return -1;
+}
+
+// v as held by wave lane `from` (ds_bpermute: a cross-lane read through the LDS crossbar that
+// touches no LDS memory). Every lane of the wave must execute it.
+__device__ __forceinline__ cf32 lane_value(cf32 v, int from)
+{
+    const int addr = from << 2;
+    return {__builtin_bit_cast(float,
+                               __builtin_amdgcn_ds_bpermute(addr, __builtin_bit_cast(int, v.re))),
+            __builtin_bit_cast(float,
+                               __builtin_amdgcn_ds_bpermute(addr, __builtin_bit_cast(int, v.im)))};
+}
+
 // Forward: z = the real arrays viewed as complex (batch x N1 x M), y = batch arrays of 2 m1 x w
 // modes. wdiv divides by w.
 template <class F>
@@ -97,28 +122,33 @@ __global__ void __launch_bounds__(F::NT)
         __builtin_amdgcn_sched_barrier(0);
     });
 
-    // Rows: transform, then X[k] = E[k] + exp(-pi i k / M) O[k] for k < w into the tile.
+    // Rows: transform, then X[k] = E[k] + exp(-pi i k / M) O[k] for k < w into the tile. The
+    // lane holds Z[k] for its k = lane + j L; the partner Z[M - k] is element (L - lane) + (E - 1
+    // - j) L, held by lane L - lane of the row (lane 0: its own element (E - j) L), and is read
+    // across lanes. Against writing the row to the scratch and reading both back (six
+    // alternated rounds over 2048 arrays, m = n / 8): 64^2 8.76 -> 8.29 us, 128^2 28.78 ->
+    // 28.32 us.
+    static_assert(F::WMax <= (PR::E - 1) * PR::L, "partners lie in the row's last E - 1 slots");
     const cf32 base = twiddle_of<2 * F::M, false>(lane);
+    const int wave_lane = tid & 63;
+    const int mirror = (wave_lane & ~(PR::L - 1)) | ((PR::L - lane) & (PR::L - 1));
     static_for<0, F::kPasses>([&](auto pi) {
         constexpr int p = decltype(pi)::value;
         run_stages<PR, 0, false, F::kTable, RowExchange<PR, F::TR>>(v[p], s, lane, table);
-        lds_sync<true>();
-        final_write<PR>(s, v[p], lane);
-        lds_sync<true>();
         cf32* const trow = tile + F::tile_row(p * F::RPP + prow);
-        static_for<0, F::WMax / PR::L + 1>([&](auto ji) {
+        static_for<0, (F::WMax + PR::L - 1) / PR::L>([&](auto ji) {
             constexpr int j = decltype(ji)::value;
+            const cf32 zk = v[p][out_slot<PR>(j)];
+            const cf32 across = lane_value(v[p][out_slot<PR>(PR::E - 1 - j)], mirror);
+            const cf32 zm = lane == 0 ? v[p][out_slot<PR>((PR::E - j) % PR::E)] : across;
             const int k = lane + j * PR::L;
             if (k < w) {
-                const cf32 zk = s[pad(k)];
-                const cf32 zm = s[pad((F::M - k) & (F::M - 1))];
                 const cf32 ev{0.5f * (zk.re + zm.re), 0.5f * (zk.im - zm.im)};
                 const cf32 od{0.5f * (zk.im + zm.im), -0.5f * (zk.re - zm.re)};
                 constexpr cf32 c = const_twiddle<false>(j * PR::L, 2 * F::M);
                 trow[k] = cadd(ev, cmul(j == 0 ? base : cmul(base, c), od));
             }
         });
-        lds_sync<true>();  // the row is read before the next pass reuses the scratch
     });
     __syncthreads();
 
