@@ -705,6 +705,31 @@ constexpr bool slots_match()
     return true;
 }
 
+// After a plan's last stage, lane l holds element l + q L of its transform (q < E) in register
+// slot out_slot<P>(q).
+template <class P>
+constexpr int out_slot(int q)
+{
+    constexpr int RL = P::template radix<P::kStages - 1>();
+    for (int e = 0; e < P::E; ++e) {
+        if ((e / RL) * P::L + (e % RL) * (P::N / RL) == q * P::L) {
+            return e;
+        }
+    }
+    return -1;
+}
+
+// v as held by wave lane `from` (ds_bpermute: a cross-lane read through the LDS crossbar that
+// touches no LDS memory). Every lane of the wave must execute it.
+__device__ __forceinline__ cf32 lane_value(cf32 v, int from)
+{
+    const int addr = from << 2;
+    return {__builtin_bit_cast(float,
+                               __builtin_amdgcn_ds_bpermute(addr, __builtin_bit_cast(int, v.re))),
+            __builtin_bit_cast(float,
+                               __builtin_amdgcn_ds_bpermute(addr, __builtin_bit_cast(int, v.im)))};
+}
+
 // Writes the last stage's outputs to LDS in natural order (for a staged store).
 template <class P, class Lay = Padded>
 __device__ __forceinline__ void final_write(cf32* s, const cf32 (&v)[P::E], int lane)
