@@ -662,8 +662,9 @@ def navier_stokes_rows(impl: str, dev, later: list) -> dict:
     trajectories, viscosity U[1e-3, 5e-3] per trajectory, Kolmogorov forcing sin(4y), dt 0.0025,
     a k^-3 Gaussian random initial vorticity from seed 0; one job = 32 physical frames 40 steps
     apart (1240 IMEX steps, frames kept on the GPU). Timed once per backend after 40 warm-up
-    steps: the fused stages (impl, pruned), this stack's composed pruned path, and, appended to
-    `later`, rocFFT pruned and rocFFT full (the reference's torch.fft comparison)."""
+    steps: the fused stages (impl, pruned; the 40 steps between frames as one launch), this
+    stack's composed pruned path, and, appended to `later`, rocFFT pruned and rocFFT full (the
+    reference's torch.fft comparison). GpuSolver.advance is step() repeated for the last three."""
     import numpy as np
     import torch
 
@@ -679,17 +680,14 @@ def navier_stokes_rows(impl: str, dev, later: list) -> dict:
 
     def run(name, kwargs):
         solver = GpuSolver(n, flow, dt, device=dev, **kwargs)
-        w_hat = solver.to_spectral(w0)
-        for _ in range(every):
-            w_hat = solver.step(w_hat)
+        w_hat = solver.advance(solver.to_spectral(w0), every)
         w_hat = solver.to_spectral(w0)
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         start.record()
         record[0] = solver.to_physical(w_hat)
         for f in range(1, frames):
-            for _ in range(every):
-                w_hat = solver.step(w_hat)
+            w_hat = solver.advance(w_hat, every)  # `every` calls of step()
             record[f] = solver.to_physical(w_hat)
         stop.record()
         stop.synchronize()

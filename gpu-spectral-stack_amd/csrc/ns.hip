@@ -184,19 +184,26 @@ __device__ __forceinline__ void pair_row_inverse(cf32* row, cf32 (&v)[NP::PX::E]
     run_stages<PX, 0, true, false>(v, row, lane, nullptr);
 }
 
-template <class NP>
-__global__ void __launch_bounds__(NP::NT)
-    ns_stage_kernel(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32* out_w,
-                    const cf32* __restrict__ forcing_hat, const float* __restrict__ nu,
-                    int nu_stride, float drag, float dt, int stage)
+// One stage of one field (the workgroup's), on the tile T. The arrays hold every field's modes;
+// `field` picks this workgroup's. out_f and out_w may overwrite state, w0 or f0 (the C ABI allows
+// it): every read of the state happens before the barrier that ends the transforms, and the
+// epilogue loads all the values a lane updates before it stores any, so those pointers are not
+// restrict. Every lane of the workgroup calls this; it starts by writing T. InLoop: the caller
+// runs stages in a loop (below).
+template <class NP, bool InLoop>
+__device__ __forceinline__ void ns_stage_body(cf32* T, long long field, const cf32* state,
+                                              const cf32* w0, const cf32* f0, cf32* out_f,
+                                              cf32* out_w, const cf32* __restrict__ forcing_hat,
+                                              float nu_f, float drag, float dt, int stage)
 {
-    // out_f and out_w may overwrite state, w0 or f0 (the C ABI allows it): every read of the
-    // state happens before the barrier that ends the transforms, and the epilogue loads all the
-    // values a lane updates before it stores any, so those pointers are not restrict.
     using PX = typename NP::PX;
-    __shared__ cf32 T[NP::kLds];
-    const int tid = threadIdx.x;
-    const long long field = blockIdx.x;
+    // In a loop, the lane index is made opaque to the optimizer, so that each stage recomputes
+    // the lane's indices and twiddles instead of keeping them live across the loop (which spilled
+    // 137 registers at n = 128).
+    int tid = threadIdx.x;
+    if constexpr (InLoop) {
+        asm volatile("" : "+v"(tid));
+    }
     const long long base = field * NP::kW;
     const cf32* const w = state + base;
     const int lane = tid % PX::L;
@@ -259,7 +266,6 @@ __global__ void __launch_bounds__(NP::NT)
 
     // Epilogue on the kept modes: every global value a lane reads is loaded before its stores.
     constexpr int kIters = (NP::kW + NP::NT - 1) / NP::NT;
-    const float nu_f = nu[field * nu_stride];
     const float kmax = static_cast<float>(NP::N) / 3.0f;
     cf32 fh[kIters];
     cf32 wv[kIters];
@@ -299,6 +305,44 @@ __global__ void __launch_bounds__(NP::NT)
     }
 }
 
+template <class NP>
+__global__ void __launch_bounds__(NP::NT)
+    ns_stage_kernel(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32* out_w,
+                    const cf32* __restrict__ forcing_hat, const float* __restrict__ nu,
+                    int nu_stride, float drag, float dt, int stage)
+{
+    __shared__ cf32 T[NP::kLds];
+    const long long field = blockIdx.x;
+    ns_stage_body<NP, false>(T, field, state, w0, f0, out_f, out_w, forcing_hat,
+                             nu[field * nu_stride], drag, dt, stage);
+}
+
+// `steps` whole steps (predictor, then corrector) per field in one launch: the field's state
+// advances in place, and its tendency and predictor go to the field's two slots of `work`. A
+// workgroup only ever reads what it wrote itself, so a barrier between the stages orders the
+// global accesses (the waves share the CU's L1), and the field's three arrays stay in its
+// XCD's L2 from one stage to the next, where separate launches write them back to HBM at the end
+// of each stage and read them again at the start of the next.
+template <class NP>
+__global__ void __launch_bounds__(NP::NT)
+    ns_steps_kernel(cf32* state, cf32* work, const cf32* __restrict__ forcing_hat,
+                    const float* __restrict__ nu, int nu_stride, float drag, float dt, int steps)
+{
+    __shared__ cf32 T[NP::kLds];
+    const long long field = blockIdx.x;
+    cf32* const tendency = work;
+    cf32* const predicted = work + static_cast<long long>(gridDim.x) * NP::kW;
+    const float nu_f = nu[field * nu_stride];
+    for (int s = 0; s < steps; ++s) {
+        ns_stage_body<NP, true>(T, field, state, nullptr, nullptr, tendency, predicted,
+                                forcing_hat, nu_f, drag, dt, 0);
+        __syncthreads();  // the predictor and tendency are written; T is free
+        ns_stage_body<NP, true>(T, field, predicted, state, tendency, nullptr, state,
+                                forcing_hat, nu_f, drag, dt, 1);
+        __syncthreads();  // the new state is written; T is free
+    }
+}
+
 template <int N>
 void launch(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32* out_w,
             const cf32* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
@@ -310,6 +354,16 @@ void launch(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32
     hipLaunchKernelGGL(ns_stage_kernel<NP>, dim3(static_cast<unsigned>(batch)), dim3(NP::NT), 0,
                        stream, state, w0, f0, out_f, out_w, forcing_hat, nu, nu_stride, drag, dt,
                        stage);
+    SPX_LAUNCH_CHECK();
+}
+
+template <int N>
+void launch_steps(cf32* state, cf32* work, const cf32* forcing_hat, const float* nu,
+                  int nu_stride, float drag, float dt, int batch, int steps, hipStream_t stream)
+{
+    using NP = std::conditional_t<N == 64, NsPairPlan<64, 8, 8>, NsPairPlan<N, 16, 16>>;
+    hipLaunchKernelGGL(ns_steps_kernel<NP>, dim3(static_cast<unsigned>(batch)), dim3(NP::NT), 0,
+                       stream, state, work, forcing_hat, nu, nu_stride, drag, dt, steps);
     SPX_LAUNCH_CHECK();
 }
 
@@ -341,6 +395,38 @@ void ns_stage(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf
     } else {
         dev::launch<128>(state, w0, f0, out_f, out_w, forcing_hat, nu, nu_stride, drag, dt,
                          batch, stage, stream);
+    }
+}
+
+void ns_steps(cf32* state, cf32* work, const cf32* forcing_hat, const float* nu, int nu_stride,
+              float drag, float dt, int n, int batch, int steps, hipStream_t stream)
+{
+    if (!ns_supports(n)) {
+        throw InvalidArgument("ns_steps: the fused Navier-Stokes stage supports n = 64 and 128, "
+                              "got " + str(n));
+    }
+    if (batch < 1 || steps < 0 || (nu_stride != 0 && nu_stride != 1)) {
+        throw InvalidArgument("ns_steps: need batch >= 1, steps >= 0, nu_stride 0 or 1");
+    }
+    if (state == nullptr || work == nullptr || forcing_hat == nullptr || nu == nullptr) {
+        throw InvalidArgument("ns_steps: state, work, forcing_hat and nu must not be null");
+    }
+    const long long m = n / 3 + 1;
+    const long long field = 2 * m * m;
+    const long long span = static_cast<long long>(batch) * field;
+    const cf32* const work_end = work + 2 * span;
+    if (state < work_end && work < state + span) {
+        throw InvalidArgument("ns_steps: work must not overlap the state");
+    }
+    if (steps == 0) {
+        return;
+    }
+    if (n == 64) {
+        dev::launch_steps<64>(state, work, forcing_hat, nu, nu_stride, drag, dt, batch, steps,
+                              stream);
+    } else {
+        dev::launch_steps<128>(state, work, forcing_hat, nu, nu_stride, drag, dt, batch, steps,
+                               stream);
     }
 }
 

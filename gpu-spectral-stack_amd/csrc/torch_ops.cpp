@@ -541,6 +541,28 @@ at::Tensor ns_correct_op(const at::Tensor& predicted, const at::Tensor& w_hat,
     return out;
 }
 
+// `steps` whole steps in one launch; returns the advanced state (the input is left as it is).
+at::Tensor ns_advance_op(const at::Tensor& w_hat, const at::Tensor& forcing_hat,
+                         const at::Tensor& nu, double drag, double dt, int64_t n, int64_t steps)
+{
+    check_ns(w_hat, forcing_hat, nu, n);
+    TORCH_CHECK(steps >= 0 && steps < (int64_t{1} << 31), "ns_advance: steps must be >= 0");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(w_hat.device());
+    at::Tensor state = w_hat.contiguous().clone();
+    const at::Tensor fh = forcing_hat.contiguous();
+    const at::Tensor nc = nu.contiguous();
+    const int64_t m = n / 3 + 1;
+    const int batch = batch_of(state, 2 * m * m, "ns_advance");
+    if (batch > 0 && steps > 0) {
+        at::Tensor work = at::empty({2, state.numel()}, state.options());
+        check_status(spx_ns_steps(mptr(state), mptr(work), cptr(fh), nc.const_data_ptr<float>(),
+                                  nc.numel() == 1 ? 0 : 1, static_cast<float>(drag),
+                                  static_cast<float>(dt), static_cast<int>(n), batch,
+                                  static_cast<int>(steps), current_stream()));
+    }
+    return state;
+}
+
 // spectral._C.fft_impls(): the registry's names, in order, as a tuple of str.
 PyObject* py_fft_impls(PyObject*, PyObject*)
 {
@@ -602,6 +624,8 @@ TORCH_LIBRARY(spectral, m)
           " -> (Tensor, Tensor)");
     m.def("ns_correct(Tensor predicted, Tensor w_hat, Tensor f0, Tensor forcing_hat, Tensor nu,"
           " float drag, float dt, int n) -> Tensor");
+    m.def("ns_advance(Tensor w_hat, Tensor forcing_hat, Tensor nu, float drag, float dt, int n,"
+          " int steps) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(spectral, CUDA, m)
@@ -621,6 +645,7 @@ TORCH_LIBRARY_IMPL(spectral, CUDA, m)
     m.impl("rf_fir_spectrum", &rf_fir_spectrum_op);
     m.impl("ns_predict", &ns_predict_op);
     m.impl("ns_correct", &ns_correct_op);
+    m.impl("ns_advance", &ns_advance_op);
 }
 
 // Importing spectral._C runs the TORCH_LIBRARY blocks (registering torch.ops.spectral) and

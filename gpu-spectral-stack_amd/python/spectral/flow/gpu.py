@@ -18,7 +18,9 @@ reference's name for the torch.fft backend, means the same.
 fused (this stack's own option): with pruned=True, a Stockham fft_impl and n = 64 or 128, each of
 a step's two stages is one kernel per field (torch.ops.spectral.ns_predict / ns_correct) holding the
 derived fields, their product and its spectrum in LDS: the arithmetic above in float32 without the
-intermediate HBM traffic. fused=None uses it wherever it applies, True requires it, False never.
+intermediate HBM traffic. advance(w, k), which frames() and simulate() use between frames, runs k
+fused steps as one launch (torch.ops.spectral.ns_advance). fused=None uses it wherever it applies,
+True requires it, False never.
 """
 
 from __future__ import annotations
@@ -177,6 +179,20 @@ class GpuSolver:
         f1 = self.tendency(predicted)
         return (carried + (0.5 * self.dt) * (f0 + f1)) * self.implicit
 
+    def advance(self, w_hat: torch.Tensor, steps: int) -> torch.Tensor:
+        """`steps` calls of step(). The fused path runs them as one launch per call (each field's
+        state, tendency and predictor stay in its XCD's L2 from stage to stage), with the same
+        arithmetic as step()."""
+        if steps < 0:
+            raise ValueError("need steps >= 0")
+        if self.fused:
+            return torch.ops.spectral.ns_advance.default(
+                w_hat, self.forcing_hat, self.nu, float(self.flow.drag), float(self.dt), self.n,
+                steps)
+        for _ in range(steps):
+            w_hat = self.step(w_hat)
+        return w_hat
+
     def frames(self, w0: torch.Tensor, steps: int, record_every: int = 1) -> Iterator[torch.Tensor]:
         """Physical vorticity at step 0 (the dealiased initial condition) and after every
         record_every steps up to `steps`, produced one at a time so a caller can stream them."""
@@ -185,11 +201,9 @@ class GpuSolver:
         w_hat = self.to_spectral(w0)
         yield self.to_physical(w_hat)
         for _ in range(steps // record_every):
-            for _ in range(record_every):
-                w_hat = self.step(w_hat)
+            w_hat = self.advance(w_hat, record_every)
             yield self.to_physical(w_hat)
-        for _ in range(steps % record_every):  # the tail past the last recorded frame
-            w_hat = self.step(w_hat)
+        self.advance(w_hat, steps % record_every)  # the tail past the last recorded frame
 
     def simulate(self, w0: torch.Tensor, steps: int, record_every: int = 1) -> torch.Tensor:
         """Every frame of frames(), stacked: (frames, ..., n, n)."""

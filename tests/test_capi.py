@@ -126,6 +126,28 @@ def test_navier_stokes_stage_arguments(lib):
     assert "stage 1 reads" in _last(lib)
 
 
+def test_navier_stokes_steps_arguments(lib):
+    # Rejected before anything reaches the device; steps = 0 is accepted and launches nothing.
+    state, work = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x200000)
+    p, f = ctypes.c_void_p(0x1000), ctypes.c_float
+    field = 2 * 22 * 22 * 8  # bytes of one 64^2 field's modes
+
+    def steps(n=64, batch=1, count=1, nu_stride=0, st=state, wk=work):
+        return lib.spx_ns_steps(st, wk, p, p, nu_stride, f(0.1), f(1e-3), n, batch, count, None)
+
+    assert steps(n=32) == SPX_EINVAL and "supports n = 64 and 128" in _last(lib)
+    assert steps(batch=0) == SPX_EINVAL and "batch >= 1" in _last(lib)
+    assert steps(count=-1) == SPX_EINVAL and "steps >= 0" in _last(lib)
+    assert steps(nu_stride=2) == SPX_EINVAL and "nu_stride 0 or 1" in _last(lib)
+    assert steps(wk=None) == SPX_EINVAL and "must not be null" in _last(lib)
+    assert steps(wk=state) == SPX_EINVAL and "must not overlap" in _last(lib)
+    # The work area's end touching the state's start, and the state's end reaching into it.
+    assert steps(wk=ctypes.c_void_p(0x100000 - 2 * field + 8)) == SPX_EINVAL
+    assert steps(wk=ctypes.c_void_p(0x100000 + field - 8)) == SPX_EINVAL
+    assert steps(wk=ctypes.c_void_p(0x100000 - 2 * field), count=0) == SPX_OK
+    assert steps(wk=ctypes.c_void_p(0x100000 + field), count=0) == SPX_OK
+
+
 def test_workspace_queries(lib):
     count = ctypes.c_size_t()
     assert lib.spx_fft2_c2c_workspace(3, 1, 8, 8, 2, ctypes.byref(count)) == SPX_OK
@@ -315,6 +337,51 @@ def test_ns_stage_may_write_over_its_inputs(lib, rng, n):
     torch.cuda.synchronize()
     assert torch.equal(over, pred) and torch.equal(f0_over, f0)
     assert torch.equal(w0, new) and torch.equal(p, new)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [64, 128])
+def test_ns_steps_equal_alternating_stages(lib, rng, n):
+    # Steps in one launch against spx_ns_stage launches into fresh outputs, to float32 rounding
+    # (the two kernels contract some products into fused multiply-adds differently: their
+    # tendencies differ in almost every mode by a few ulps, and each is as far from the composed
+    # float32 path as the other, 2-6e-6), with the state advanced in place and the work area
+    # holding the last step's tendency and predictor. The tendency, a difference of the forcing
+    # and the nonlinear term, carries the larger relative rounding. The launch is deterministic:
+    # a second run from the same state gives the same bits.
+    from spectral.flow import Flow
+    from spectral.flow.gpu import GpuSolver
+
+    solver = GpuSolver(n, Flow(viscosity=np.array([1e-3, 4e-3, 2e-3])), 2.5e-3, pruned=True)
+    w = solver.to_spectral(torch.from_numpy(rng.standard_normal((3, n, n))).float().cuda())
+    args = (_ptr(solver.forcing_hat), ctypes.c_void_p(solver.nu.data_ptr()), 1,
+            ctypes.c_float(0.1), ctypes.c_float(2.5e-3), n, 3)
+
+    def rel(a, b):
+        return float(torch.linalg.vector_norm(a - b) / torch.linalg.vector_norm(b))
+
+    state, done = w, 0
+    for steps, bound in ((1, 1e-6), (4, 1e-5)):  # the state's and the predictor's
+        while done < steps:
+            f0, pred, new = torch.empty_like(w), torch.empty_like(w), torch.empty_like(w)
+            assert lib.spx_ns_stage(_ptr(state), None, None, _ptr(f0), _ptr(pred), *args, 0,
+                                    None) == SPX_OK
+            assert lib.spx_ns_stage(_ptr(pred), _ptr(state), _ptr(f0), None, _ptr(new), *args,
+                                    1, None) == SPX_OK
+            state, done = new, done + 1
+        runs = []
+        for _ in range(2):
+            advanced = w.clone()
+            work = torch.full((2,) + tuple(w.shape), float("nan"), dtype=w.dtype,
+                              device=w.device)
+            assert lib.spx_ns_steps(_ptr(advanced), _ptr(work), *args, steps, None) == SPX_OK
+            runs.append((advanced, work))
+        torch.cuda.synchronize()
+        (advanced, work), (again, work_again) = runs
+        assert torch.equal(advanced, again) and torch.equal(work, work_again)
+        assert rel(advanced, state) < bound, f"{steps} steps"
+        assert rel(work[1], pred) < bound, f"{steps} steps"
+        assert rel(work[0], f0) < 2e-5, f"{steps} steps"
 
 
 def _fft_columns(x: np.ndarray, inverse: bool) -> np.ndarray:

@@ -1,7 +1,9 @@
 """The fused Navier-Stokes stages (torch.ops.spectral.ns_predict / ns_correct, C ABI spx_ns_stage):
 one kernel per field and stage, against the composed GpuSolver path on the same state, against the
 float64 oracle over many steps, and against the exact Taylor-Green and laminar Kolmogorov
-solutions and the energy budget of the truncated system."""
+solutions and the energy budget of the truncated system. The many-step launch
+(torch.ops.spectral.ns_advance, C ABI spx_ns_steps, GpuSolver.advance) against the same steps
+taken one stage at a time."""
 
 import numpy as np
 import pytest
@@ -165,3 +167,73 @@ def test_operators_reject_bad_arguments(rng):
         torch.ops.spectral.ns_predict(w, fh, nu.double(), 0.1, 1e-3, n)
     with pytest.raises(RuntimeError, match="same shape"):
         torch.ops.spectral.ns_correct(w, w[:1], w, fh, nu, 0.1, 1e-3, n)
+    with pytest.raises(RuntimeError, match="steps must be >= 0"):
+        torch.ops.spectral.ns_advance(w, fh, nu, 0.1, 1e-3, n, -1)
+    with pytest.raises(ValueError, match="steps >= 0"):
+        solver.advance(w, -1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", SIZES)
+@pytest.mark.parametrize("viscosity", [np.array([1e-3, 4e-3, 2e-2]), 3e-3],
+                         ids=["per-field", "shared"])
+def test_advance_equals_the_stages_one_at_a_time(rng, n, viscosity):
+    # The many-step kernel runs the stage kernel's code on the same values; the compiler may
+    # contract a few products into fused multiply-adds differently in the two kernels, so the
+    # states agree to float32 rounding after every count of steps (none: exactly).
+    dt = 2.5e-3
+    solver = GpuSolver(n, Flow(viscosity=viscosity, drag=0.1), dt, pruned=True, fused=True)
+    w = random_state(rng, n, (3,), solver)
+    stepped, done = w, 0
+    for steps in (0, 1, 2, 5):
+        while done < steps:
+            f0, predicted = torch.ops.spectral.ns_predict(stepped, solver.forcing_hat, solver.nu,
+                                                          0.1, dt, n)
+            stepped = torch.ops.spectral.ns_correct(predicted, stepped, f0, solver.forcing_hat,
+                                                    solver.nu, 0.1, dt, n)
+            done += 1
+        advanced = solver.advance(w, steps)
+        assert advanced.data_ptr() != w.data_ptr()
+        if steps == 0:
+            assert torch.equal(advanced, w)
+        else:
+            assert relative(advanced, stepped) < 1e-6, f"{steps} steps"
+
+
+@pytest.mark.gpu
+def test_advance_keeps_its_input_and_batch_shapes(rng):
+    n, dt = 128, 2.5e-3
+    fused = GpuSolver(n, Flow(viscosity=3e-3), dt, pruned=True, fused=True)
+    composed = GpuSolver(n, Flow(viscosity=3e-3), dt, pruned=True, fused=False)
+    w = random_state(rng, n, (2, 3), composed)
+    kept = w.clone()
+    out = fused.advance(w, 4)
+    assert torch.equal(w, kept) and out.shape == w.shape
+    expected = w
+    for _ in range(4):
+        expected = composed.step(expected)
+    assert relative(out, expected) < 1e-5
+    # A non-contiguous state is read through a contiguous copy; an empty batch launches nothing.
+    wt = w.transpose(0, 1)
+    assert torch.equal(fused.advance(wt, 2), fused.advance(wt.contiguous(), 2))  # same launch
+    assert fused.advance(w[:0], 3).shape == w[:0].shape
+
+
+@pytest.mark.gpu
+def test_frames_take_the_many_step_path(rng):
+    # frames() advances between frames with advance(); the frames equal those of step() calls.
+    n, dt = 64, 2.5e-3
+    solver = GpuSolver(n, Flow(viscosity=np.array([2e-3, 5e-3])), dt, pruned=True, fused=True)
+    w0 = torch.as_tensor(ref.smooth_random_field(rng, n, batch=(2,)), dtype=torch.float32,
+                         device="cuda")
+    frames = list(solver.frames(w0, 7, record_every=3))
+    assert len(frames) == 3
+    w_hat = solver.to_spectral(w0)
+    expected = [solver.to_physical(w_hat)]
+    for _ in range(2):
+        for _ in range(3):
+            w_hat = solver.step(w_hat)
+        expected.append(solver.to_physical(w_hat))
+    assert torch.equal(frames[0], expected[0])
+    for got, want in zip(frames[1:], expected[1:]):
+        assert relative(got, want) < 1e-6
