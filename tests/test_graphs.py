@@ -124,6 +124,14 @@ def test_fused_navier_stokes_steps_under_capture(rng):
     replay_matches_eager(steps, fields)
 
 
+@pytest.mark.parametrize("n", [64, 128])
+def test_navier_stokes_many_step_launch_under_capture(rng, n):
+    solver = GpuSolver(n, Flow(viscosity=np.array([1e-3, 3e-3, 5e-3])), 0.0025,
+                       fft_impl="stockham_r8", pruned=True)
+    fields = [solver.to_spectral(cuda(random_real(rng, (3, n, n)))) for _ in range(3)]
+    replay_matches_eager(lambda w_hat: solver.advance(w_hat, 6), fields)
+
+
 @pytest.mark.parametrize(("n", "batch"), [(1 << 20, 2), (1 << 22, 1)])
 def test_large_c2c_without_allocation_under_capture(rng, n, batch):
     # Beyond 16384 points spx_c2c takes stream-ordered scratch; spx_c2c_noalloc, the entry point
