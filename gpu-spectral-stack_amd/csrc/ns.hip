@@ -38,6 +38,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <type_traits>
 
 namespace spx {
@@ -411,11 +412,11 @@ void ns_steps(cf32* state, cf32* work, const cf32* forcing_hat, const float* nu,
     if (state == nullptr || work == nullptr || forcing_hat == nullptr || nu == nullptr) {
         throw InvalidArgument("ns_steps: state, work, forcing_hat and nu must not be null");
     }
-    const long long m = n / 3 + 1;
-    const long long field = 2 * m * m;
-    const long long span = static_cast<long long>(batch) * field;
-    const cf32* const work_end = work + 2 * span;
-    if (state < work_end && work < state + span) {
+    const auto m = static_cast<std::uintptr_t>(n / 3 + 1);
+    const std::uintptr_t bytes = static_cast<std::uintptr_t>(batch) * 2 * m * m * sizeof(cf32);
+    const auto s0 = reinterpret_cast<std::uintptr_t>(state);
+    const auto w0 = reinterpret_cast<std::uintptr_t>(work);
+    if (s0 < w0 + 2 * bytes && w0 < s0 + bytes) {
         throw InvalidArgument("ns_steps: work must not overlap the state");
     }
     if (steps == 0) {

@@ -546,7 +546,8 @@ at::Tensor ns_advance_op(const at::Tensor& w_hat, const at::Tensor& forcing_hat,
                          const at::Tensor& nu, double drag, double dt, int64_t n, int64_t steps)
 {
     check_ns(w_hat, forcing_hat, nu, n);
-    TORCH_CHECK(steps >= 0 && steps < (int64_t{1} << 31), "ns_advance: steps must be >= 0");
+    TORCH_CHECK(steps >= 0 && steps < (int64_t{1} << 31),
+                "ns_advance: steps must be >= 0 and below 2^31, got ", steps);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(w_hat.device());
     at::Tensor state = w_hat.contiguous().clone();
     const at::Tensor fh = forcing_hat.contiguous();
