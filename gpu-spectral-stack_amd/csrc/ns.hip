@@ -3,6 +3,9 @@
 // LDS and registers. This is the MI355X form of the reference's GpuSolver.tendency / step
 // (python/spectral/flow/gpu.py:115-129), which runs one batched inverse transform of four fields,
 // a product, a forward transform and about fifteen elementwise kernels through HBM per tendency.
+// ns_steps_kernel runs the same stage body for many steps per launch (a field's steps depend only
+// on that field), in place of the reference's one Python-driven step per call
+// (python/spectral/flow/gpu.py:125-142).
 //
 // State: omega_hat on the 2/3-rule modes in the layout of rfft2_truncated with m = n/3 + 1 (rows
 // ky = 0 .. m-1 then -m .. -1, columns kx = 0 .. m-1), (2m) x m complex values per field.
