@@ -3,8 +3,11 @@ with sizes, batch counts, implementations and column methods drawn at random wit
 limits. The hand-picked tests elsewhere pin each kernel's edges; this sample reaches the
 combinations between them (odd batch counts against each plan's transforms per workgroup and
 the persistent kernels' resident grid, flat and tall 2D shapes, pruned bounds), as a guard
-against a case that none of them names. The sample is drawn once at collection from a fixed
-seed, so every run checks the same cases, each under its own test id."""
+against a case that none of them names. The radio callers and the Navier-Stokes many-step launch
+(random grid, field count across several workgroups per compute unit, step count, shared or
+per-field viscosity; against step() repeated) get samples of their own. Every sample is drawn
+once at collection from a fixed seed, so every run checks the same cases, each under its own
+test id."""
 
 import numpy as np
 import pytest
@@ -236,6 +239,46 @@ def test_random_radio_case_matches_the_oracle(rng, case):
         assert rel_l2(y, filtered(x, taps)) < 2e-5
 
 
+# --- the Navier-Stokes caller: many steps per launch -------------------------------------------
+
+def _draw_flow_cases() -> list[tuple]:
+    draw = np.random.default_rng(20261204)
+    cases = []
+    for _ in range(12):
+        n = [64, 128][int(draw.integers(2))]
+        batch = int(draw.integers(1, 600))  # up to more than two workgroups per compute unit
+        steps = int(draw.integers(0, 6))
+        shared = bool(draw.integers(2))
+        cases.append((n, batch, steps, shared))
+    return cases
+
+
+FLOW_CASES = _draw_flow_cases()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", FLOW_CASES,
+                         ids=[f"ns{n}-b{b}-s{k}-{'shared' if sh else 'per-field'}"
+                              for n, b, k, sh in FLOW_CASES])
+def test_random_flow_case_matches_the_stages(rng, case):
+    from spectral.flow import Flow
+    from spectral.flow.gpu import GpuSolver
+
+    n, batch, steps, shared = case
+    viscosity = 2e-3 if shared else rng.uniform(1e-3, 5e-3, batch)
+    solver = GpuSolver(n, Flow(viscosity=viscosity), 2.5e-3, pruned=True, fused=True)
+    w = solver.to_spectral(dev(random_real(rng, (batch, n, n))))
+    expected = w
+    for _ in range(steps):
+        expected = solver.step(expected)
+    got = solver.advance(w, steps)
+    if steps == 0:
+        assert torch.equal(got, w)
+    else:
+        err = torch.linalg.vector_norm(got - expected) / torch.linalg.vector_norm(expected)
+        assert float(err) < 1e-5
+
+
 def test_the_sample_covers_every_operator_and_implementation():
     ops = {c[0] for c in CASES}
     impls = {c[1] for c in CASES}
@@ -243,3 +286,5 @@ def test_the_sample_covers_every_operator_and_implementation():
     assert set(STOCKHAM) <= impls and "naive" in impls
     assert all(c[2] in ("strided", "transpose", "auto") for c in CASES if c[0] in ("fft2", "real2"))
     assert {c[0] for c in RADIO_CASES} == {"spectrum", "fir"}
+    assert {c[0] for c in FLOW_CASES} == {64, 128} and max(c[1] for c in FLOW_CASES) > 512
+    assert {c[2] for c in FLOW_CASES} >= {0, 1} and {c[3] for c in FLOW_CASES} == {True, False}
