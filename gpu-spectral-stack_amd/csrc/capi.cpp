@@ -346,13 +346,13 @@ int spx_ns_stage(const void* state, const void* w0, const void* f0, void* out_f,
     });
 }
 
-int spx_ns_steps(void* state, void* work, const void* forcing_hat, const float* nu,
-                 int nu_stride, float drag, float dt, int n, int batch, int steps,
-                 hipStream_t stream)
+int spx_ns_steps(const void* w_in, void* w_out, void* work, const void* forcing_hat,
+                 const float* nu, int nu_stride, float drag, float dt, int n, int batch,
+                 int steps, hipStream_t stream)
 {
     return guarded([&] {
-        spx::ns_steps(cm(state), cm(work), cc(forcing_hat), nu, nu_stride, drag, dt, n, batch,
-                      steps, stream);
+        spx::ns_steps(cc(w_in), cm(w_out), cm(work), cc(forcing_hat), nu, nu_stride, drag, dt, n,
+                      batch, steps, stream);
     });
 }
 

@@ -239,10 +239,11 @@ bool ns_supports(int n);
 void ns_stage(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32* out_w,
               const cf32* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
               int n, int batch, int stage, hipStream_t stream);
-// `steps` whole steps in one launch, the state advanced in place; work holds 2 batch (2m) m
-// values (each field's tendency and predictor).
-void ns_steps(cf32* state, cf32* work, const cf32* forcing_hat, const float* nu, int nu_stride,
-              float drag, float dt, int n, int batch, int steps, hipStream_t stream);
+// `steps` whole steps in one launch from w_in to w_out (the same array, or disjoint ones); work
+// holds 2 batch (2m) m values (each field's tendency and predictor).
+void ns_steps(const cf32* w_in, cf32* w_out, cf32* work, const cf32* forcing_hat,
+              const float* nu, int nu_stride, float drag, float dt, int n, int batch, int steps,
+              hipStream_t stream);
 
 }  // namespace spx
 

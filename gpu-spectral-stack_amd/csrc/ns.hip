@@ -321,16 +321,18 @@ __global__ void __launch_bounds__(NP::NT)
                              nu[field * nu_stride], drag, dt, stage);
 }
 
-// `steps` whole steps (predictor, then corrector) per field in one launch: the field's state
-// advances in place, and its tendency and predictor go to the field's two slots of `work`. A
+// `steps` whole steps (predictor, then corrector) per field in one launch: the first step reads
+// w_in and writes w_out, the later ones advance w_out in place (w_in may be w_out), and each
+// step's tendency and predictor go to the field's two slots of `work`. A
 // workgroup only ever reads what it wrote itself, so a barrier between the stages orders the
 // global accesses (the waves share the CU's L1), and the field's three arrays stay in its
 // XCD's L2 from one stage to the next, where separate launches write them back to HBM at the end
 // of each stage and read them again at the start of the next.
 template <class NP>
 __global__ void __launch_bounds__(NP::NT)
-    ns_steps_kernel(cf32* state, cf32* work, const cf32* __restrict__ forcing_hat,
-                    const float* __restrict__ nu, int nu_stride, float drag, float dt, int steps)
+    ns_steps_kernel(const cf32* w_in, cf32* w_out, cf32* work,
+                    const cf32* __restrict__ forcing_hat, const float* __restrict__ nu,
+                    int nu_stride, float drag, float dt, int steps)
 {
     __shared__ cf32 T[NP::kLds];
     const long long field = blockIdx.x;
@@ -338,10 +340,11 @@ __global__ void __launch_bounds__(NP::NT)
     cf32* const predicted = work + static_cast<long long>(gridDim.x) * NP::kW;
     const float nu_f = nu[field * nu_stride];
     for (int s = 0; s < steps; ++s) {
+        const cf32* const state = s == 0 ? w_in : w_out;
         ns_stage_body<NP, true>(T, field, state, nullptr, nullptr, tendency, predicted,
                                 forcing_hat, nu_f, drag, dt, 0);
         __syncthreads();  // the predictor and tendency are written; T is free
-        ns_stage_body<NP, true>(T, field, predicted, state, tendency, nullptr, state,
+        ns_stage_body<NP, true>(T, field, predicted, state, tendency, nullptr, w_out,
                                 forcing_hat, nu_f, drag, dt, 1);
         __syncthreads();  // the new state is written; T is free
     }
@@ -362,12 +365,13 @@ void launch(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf32
 }
 
 template <int N>
-void launch_steps(cf32* state, cf32* work, const cf32* forcing_hat, const float* nu,
-                  int nu_stride, float drag, float dt, int batch, int steps, hipStream_t stream)
+void launch_steps(const cf32* w_in, cf32* w_out, cf32* work, const cf32* forcing_hat,
+                  const float* nu, int nu_stride, float drag, float dt, int batch, int steps,
+                  hipStream_t stream)
 {
     using NP = std::conditional_t<N == 64, NsPairPlan<64, 8, 8>, NsPairPlan<N, 16, 16>>;
     hipLaunchKernelGGL(ns_steps_kernel<NP>, dim3(static_cast<unsigned>(batch)), dim3(NP::NT), 0,
-                       stream, state, work, forcing_hat, nu, nu_stride, drag, dt, steps);
+                       stream, w_in, w_out, work, forcing_hat, nu, nu_stride, drag, dt, steps);
     SPX_LAUNCH_CHECK();
 }
 
@@ -402,8 +406,9 @@ void ns_stage(const cf32* state, const cf32* w0, const cf32* f0, cf32* out_f, cf
     }
 }
 
-void ns_steps(cf32* state, cf32* work, const cf32* forcing_hat, const float* nu, int nu_stride,
-              float drag, float dt, int n, int batch, int steps, hipStream_t stream)
+void ns_steps(const cf32* w_in, cf32* w_out, cf32* work, const cf32* forcing_hat,
+              const float* nu, int nu_stride, float drag, float dt, int n, int batch, int steps,
+              hipStream_t stream)
 {
     if (!ns_supports(n)) {
         throw InvalidArgument("ns_steps: the fused Navier-Stokes stage supports n = 64 and 128, "
@@ -412,25 +417,35 @@ void ns_steps(cf32* state, cf32* work, const cf32* forcing_hat, const float* nu,
     if (batch < 1 || steps < 0 || (nu_stride != 0 && nu_stride != 1)) {
         throw InvalidArgument("ns_steps: need batch >= 1, steps >= 0, nu_stride 0 or 1");
     }
-    if (state == nullptr || work == nullptr || forcing_hat == nullptr || nu == nullptr) {
-        throw InvalidArgument("ns_steps: state, work, forcing_hat and nu must not be null");
+    if (w_in == nullptr || w_out == nullptr || work == nullptr || forcing_hat == nullptr ||
+        nu == nullptr) {
+        throw InvalidArgument("ns_steps: w_in, w_out, work, forcing_hat and nu must not be null");
     }
     const auto m = static_cast<std::uintptr_t>(n / 3 + 1);
     const std::uintptr_t bytes = static_cast<std::uintptr_t>(batch) * 2 * m * m * sizeof(cf32);
-    const auto s0 = reinterpret_cast<std::uintptr_t>(state);
-    const auto w0 = reinterpret_cast<std::uintptr_t>(work);
-    if (s0 < w0 + 2 * bytes && w0 < s0 + bytes) {
-        throw InvalidArgument("ns_steps: work must not overlap the state");
+    const auto in = reinterpret_cast<std::uintptr_t>(w_in);
+    const auto out = reinterpret_cast<std::uintptr_t>(w_out);
+    const auto wk = reinterpret_cast<std::uintptr_t>(work);
+    const auto overlap = [](std::uintptr_t a, std::uintptr_t a_bytes, std::uintptr_t b,
+                            std::uintptr_t b_bytes) { return a < b + b_bytes && b < a + a_bytes; };
+    if (overlap(wk, 2 * bytes, in, bytes) || overlap(wk, 2 * bytes, out, bytes)) {
+        throw InvalidArgument("ns_steps: work must not overlap w_in or w_out");
+    }
+    if (in != out && overlap(in, bytes, out, bytes)) {
+        throw InvalidArgument("ns_steps: w_in and w_out must be the same array or not overlap");
     }
     if (steps == 0) {
+        if (in != out) {
+            SPX_HIP_CHECK(hipMemcpyAsync(w_out, w_in, bytes, hipMemcpyDeviceToDevice, stream));
+        }
         return;
     }
     if (n == 64) {
-        dev::launch_steps<64>(state, work, forcing_hat, nu, nu_stride, drag, dt, batch, steps,
-                              stream);
+        dev::launch_steps<64>(w_in, w_out, work, forcing_hat, nu, nu_stride, drag, dt, batch,
+                              steps, stream);
     } else {
-        dev::launch_steps<128>(state, work, forcing_hat, nu, nu_stride, drag, dt, batch, steps,
-                               stream);
+        dev::launch_steps<128>(w_in, w_out, work, forcing_hat, nu, nu_stride, drag, dt, batch,
+                               steps, stream);
     }
 }
 

@@ -541,7 +541,7 @@ at::Tensor ns_correct_op(const at::Tensor& predicted, const at::Tensor& w_hat,
     return out;
 }
 
-// `steps` whole steps in one launch; returns the advanced state (the input is left as it is).
+// `steps` whole steps in one launch into a new tensor (the input is left as it is).
 at::Tensor ns_advance_op(const at::Tensor& w_hat, const at::Tensor& forcing_hat,
                          const at::Tensor& nu, double drag, double dt, int64_t n, int64_t steps)
 {
@@ -549,19 +549,21 @@ at::Tensor ns_advance_op(const at::Tensor& w_hat, const at::Tensor& forcing_hat,
     TORCH_CHECK(steps >= 0 && steps < (int64_t{1} << 31),
                 "ns_advance: steps must be >= 0 and below 2^31, got ", steps);
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(w_hat.device());
-    at::Tensor state = w_hat.contiguous().clone();
+    const at::Tensor w = w_hat.contiguous();
     const at::Tensor fh = forcing_hat.contiguous();
     const at::Tensor nc = nu.contiguous();
+    at::Tensor out = at::empty_like(w);
     const int64_t m = n / 3 + 1;
-    const int batch = batch_of(state, 2 * m * m, "ns_advance");
-    if (batch > 0 && steps > 0) {
-        at::Tensor work = at::empty({2, state.numel()}, state.options());
-        check_status(spx_ns_steps(mptr(state), mptr(work), cptr(fh), nc.const_data_ptr<float>(),
-                                  nc.numel() == 1 ? 0 : 1, static_cast<float>(drag),
-                                  static_cast<float>(dt), static_cast<int>(n), batch,
-                                  static_cast<int>(steps), current_stream()));
+    const int batch = batch_of(w, 2 * m * m, "ns_advance");
+    if (batch > 0) {
+        at::Tensor work = at::empty({2, w.numel()}, w.options());
+        check_status(spx_ns_steps(cptr(w), mptr(out), mptr(work), cptr(fh),
+                                  nc.const_data_ptr<float>(), nc.numel() == 1 ? 0 : 1,
+                                  static_cast<float>(drag), static_cast<float>(dt),
+                                  static_cast<int>(n), batch, static_cast<int>(steps),
+                                  current_stream()));
     }
-    return state;
+    return out;
 }
 
 // spectral._C.fft_impls(): the registry's names, in order, as a tuple of str.

@@ -15,12 +15,13 @@ real 2D transforms. The API, options and discretization are the reference's
 fft_impl names one of spectral.FFT_IMPLS, or "rocfft" for torch.fft (rocFFT on ROCm); "cufft", the
 reference's name for the torch.fft backend, means the same.
 
-fused (this stack's own option): with pruned=True, a Stockham fft_impl and n = 64 or 128, each of
-a step's two stages is one kernel per field (torch.ops.spectral.ns_predict / ns_correct) holding the
-derived fields, their product and its spectrum in LDS: the arithmetic above in float32 without the
-intermediate HBM traffic. advance(w, k), which frames() and simulate() use between frames, runs k
-fused steps as one launch (torch.ops.spectral.ns_advance). fused=None uses it wherever it applies,
-True requires it, False never.
+fused (this stack's own option): with pruned=True, a Stockham fft_impl and n = 64 or 128, a field's
+step is one workgroup running both stages, each holding the derived fields, their product and its
+spectrum in LDS: the arithmetic above in float32 without the intermediate HBM traffic. step() is
+one launch (torch.ops.spectral.ns_advance with one step); advance(w, k), which frames() and
+simulate() use between frames, runs k steps as one launch. The single stages are also exposed
+(torch.ops.spectral.ns_predict / ns_correct). fused=None uses it wherever it applies, True
+requires it, False never.
 """
 
 from __future__ import annotations
@@ -166,13 +167,7 @@ class GpuSolver:
 
     def step(self, w_hat: torch.Tensor) -> torch.Tensor:
         if self.fused:
-            drag, dt, n = float(self.flow.drag), float(self.dt), self.n
-            f0, predicted = torch.ops.spectral.ns_predict.default(
-                w_hat, self.forcing_hat, self.nu, drag, dt, n
-            )
-            return torch.ops.spectral.ns_correct.default(
-                predicted, w_hat, f0, self.forcing_hat, self.nu, drag, dt, n
-            )
+            return self.advance(w_hat, 1)
         carried = self.explicit * w_hat
         f0 = self.tendency(w_hat)
         predicted = (carried + self.dt * f0) * self.implicit
@@ -180,8 +175,8 @@ class GpuSolver:
         return (carried + (0.5 * self.dt) * (f0 + f1)) * self.implicit
 
     def advance(self, w_hat: torch.Tensor, steps: int) -> torch.Tensor:
-        """`steps` calls of step(). The fused path runs them as one launch per call (each field's
-        state, tendency and predictor stay in its XCD's L2 from stage to stage), with the same
+        """`steps` calls of step(). The fused path runs them as one launch (each field's state,
+        tendency and predictor stay in its XCD's L2 from stage to stage), with the same
         arithmetic as step()."""
         if steps < 0:
             raise ValueError("need steps >= 0")

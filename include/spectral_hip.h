@@ -163,14 +163,16 @@ int spx_ns_stage(const void* state, const void* w0, const void* f0, void* out_f,
                  const void* forcing_hat, const float* nu, int nu_stride, float drag, float dt,
                  int n, int batch, int stage, hipStream_t stream);
 /* spx_ns_steps: `steps` whole steps (stage 0, then stage 1, as spx_ns_stage computes them) of
- * every field in one launch, the same arithmetic as alternating spx_ns_stage calls. `state`
- * ((2m) x m modes per field) is advanced in place. `work` holds 2 * batch * (2m) * m complex
- * values (each field's tendency and predictor) and must not overlap the state or forcing_hat.
- * steps = 0 leaves the state as it is. No counterpart in the reference: its solver launches
- * every step's kernels from Python (python/spectral/flow/gpu.py:125-142). */
-int spx_ns_steps(void* state, void* work, const void* forcing_hat, const float* nu,
-                 int nu_stride, float drag, float dt, int n, int batch, int steps,
-                 hipStream_t stream);
+ * every field in one launch, to float32 rounding the arithmetic of alternating spx_ns_stage
+ * calls. The first step reads w_in and writes w_out; later steps advance w_out in place. w_in and
+ * w_out ((2m) x m modes per field) are the same array or do not overlap. `work` holds
+ * 2 * batch * (2m) * m complex values (each field's tendency and predictor; after the call, the
+ * last step's) and overlaps neither, nor forcing_hat. steps = 0 copies w_in to w_out. No
+ * counterpart in the reference: its solver launches every step's kernels from Python
+ * (python/spectral/flow/gpu.py:125-142). */
+int spx_ns_steps(const void* w_in, void* w_out, void* work, const void* forcing_hat,
+                 const float* nu, int nu_stride, float drag, float dt, int n, int batch,
+                 int steps, hipStream_t stream);
 
 /* --- the radio callers -------------------------------------------------------------------
  * No counterpart in the reference's FFI: its rf.spectrum and rf.fir (python/spectral/rf.py:94-153)

@@ -127,25 +127,33 @@ def test_navier_stokes_stage_arguments(lib):
 
 
 def test_navier_stokes_steps_arguments(lib):
-    # Rejected before anything reaches the device; steps = 0 is accepted and launches nothing.
-    state, work = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x200000)
+    # Rejected before anything reaches the device; steps = 0 in place is accepted and queues
+    # nothing.
+    state, work = 0x100000, 0x200000
     p, f = ctypes.c_void_p(0x1000), ctypes.c_float
     field = 2 * 22 * 22 * 8  # bytes of one 64^2 field's modes
+    v = ctypes.c_void_p
 
-    def steps(n=64, batch=1, count=1, nu_stride=0, st=state, wk=work):
-        return lib.spx_ns_steps(st, wk, p, p, nu_stride, f(0.1), f(1e-3), n, batch, count, None)
+    def steps(n=64, batch=1, count=1, nu_stride=0, w_in=state, w_out=state, wk=work):
+        return lib.spx_ns_steps(v(w_in), v(w_out), v(wk), p, p, nu_stride, f(0.1), f(1e-3), n,
+                                batch, count, None)
 
     assert steps(n=32) == SPX_EINVAL and "supports n = 64 and 128" in _last(lib)
     assert steps(batch=0) == SPX_EINVAL and "batch >= 1" in _last(lib)
     assert steps(count=-1) == SPX_EINVAL and "steps >= 0" in _last(lib)
     assert steps(nu_stride=2) == SPX_EINVAL and "nu_stride 0 or 1" in _last(lib)
     assert steps(wk=None) == SPX_EINVAL and "must not be null" in _last(lib)
+    assert steps(w_out=None) == SPX_EINVAL and "must not be null" in _last(lib)
     assert steps(wk=state) == SPX_EINVAL and "must not overlap" in _last(lib)
-    # The work area's end touching the state's start, and the state's end reaching into it.
-    assert steps(wk=ctypes.c_void_p(0x100000 - 2 * field + 8)) == SPX_EINVAL
-    assert steps(wk=ctypes.c_void_p(0x100000 + field - 8)) == SPX_EINVAL
-    assert steps(wk=ctypes.c_void_p(0x100000 - 2 * field), count=0) == SPX_OK
-    assert steps(wk=ctypes.c_void_p(0x100000 + field), count=0) == SPX_OK
+    # The work area's end reaching into the state, the state's end into the work area, and the
+    # work area over a separate output.
+    assert steps(wk=state - 2 * field + 8) == SPX_EINVAL
+    assert steps(wk=state + field - 8) == SPX_EINVAL
+    assert steps(w_out=work + 8) == SPX_EINVAL and "overlap w_in or w_out" in _last(lib)
+    # Input and output: the same array, or apart; a partial overlap is refused.
+    assert steps(w_out=state + 8) == SPX_EINVAL and "the same array" in _last(lib)
+    assert steps(wk=state - 2 * field, count=0) == SPX_OK
+    assert steps(wk=state + field, count=0) == SPX_OK
 
 
 def test_workspace_queries(lib):
@@ -345,15 +353,16 @@ def test_ns_steps_equal_alternating_stages(lib, rng, n):
     # Steps in one launch against spx_ns_stage launches into fresh outputs, to float32 rounding
     # (the two kernels contract some products into fused multiply-adds differently: their
     # tendencies differ in almost every mode by a few ulps, and each is as far from the composed
-    # float32 path as the other, 2-6e-6), with the state advanced in place and the work area
-    # holding the last step's tendency and predictor. The tendency, a difference of the forcing
-    # and the nonlinear term, carries the larger relative rounding. The launch is deterministic:
-    # a second run from the same state gives the same bits.
+    # float32 path as the other, 2-6e-6), out of place and in place, with the work area holding
+    # the last step's tendency and predictor. The tendency, a difference of the forcing and the
+    # nonlinear term, carries the larger relative rounding. The launch is deterministic: every
+    # run from the same state gives the same bits, in place or not.
     from spectral.flow import Flow
     from spectral.flow.gpu import GpuSolver
 
     solver = GpuSolver(n, Flow(viscosity=np.array([1e-3, 4e-3, 2e-3])), 2.5e-3, pruned=True)
     w = solver.to_spectral(torch.from_numpy(rng.standard_normal((3, n, n))).float().cuda())
+    kept = w.clone()
     args = (_ptr(solver.forcing_hat), ctypes.c_void_p(solver.nu.data_ptr()), 1,
             ctypes.c_float(0.1), ctypes.c_float(2.5e-3), n, 3)
 
@@ -370,18 +379,27 @@ def test_ns_steps_equal_alternating_stages(lib, rng, n):
                                     1, None) == SPX_OK
             state, done = new, done + 1
         runs = []
-        for _ in range(2):
-            advanced = w.clone()
+        for in_place in (False, True, False):
+            out = w.clone() if in_place else torch.full_like(w, float("nan"))
             work = torch.full((2,) + tuple(w.shape), float("nan"), dtype=w.dtype,
                               device=w.device)
-            assert lib.spx_ns_steps(_ptr(advanced), _ptr(work), *args, steps, None) == SPX_OK
-            runs.append((advanced, work))
+            source = out if in_place else w
+            assert lib.spx_ns_steps(_ptr(source), _ptr(out), _ptr(work), *args, steps,
+                                    None) == SPX_OK
+            runs.append((out, work))
         torch.cuda.synchronize()
-        (advanced, work), (again, work_again) = runs
-        assert torch.equal(advanced, again) and torch.equal(work, work_again)
-        assert rel(advanced, state) < bound, f"{steps} steps"
+        assert torch.equal(w, kept)
+        (out, work) = runs[0]
+        for again, work_again in runs[1:]:
+            assert torch.equal(out, again) and torch.equal(work, work_again)
+        assert rel(out, state) < bound, f"{steps} steps"
         assert rel(work[1], pred) < bound, f"{steps} steps"
         assert rel(work[0], f0) < 2e-5, f"{steps} steps"
+    # No steps: a copy.
+    out = torch.full_like(w, float("nan"))
+    assert lib.spx_ns_steps(_ptr(w), _ptr(out), _ptr(work), *args, 0, None) == SPX_OK
+    torch.cuda.synchronize()
+    assert torch.equal(out, w)
 
 
 def _fft_columns(x: np.ndarray, inverse: bool) -> np.ndarray:

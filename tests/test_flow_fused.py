@@ -221,7 +221,9 @@ def test_advance_keeps_its_input_and_batch_shapes(rng):
 
 @pytest.mark.gpu
 def test_frames_take_the_many_step_path(rng):
-    # frames() advances between frames with advance(); the frames equal those of step() calls.
+    # frames() advances between frames with advance(); step() is advance() by one step, and the
+    # many-step kernel does the same arithmetic every step, so the frames equal those of step()
+    # calls bit for bit.
     n, dt = 64, 2.5e-3
     solver = GpuSolver(n, Flow(viscosity=np.array([2e-3, 5e-3])), dt, pruned=True, fused=True)
     w0 = torch.as_tensor(ref.smooth_random_field(rng, n, batch=(2,)), dtype=torch.float32,
@@ -234,6 +236,5 @@ def test_frames_take_the_many_step_path(rng):
         for _ in range(3):
             w_hat = solver.step(w_hat)
         expected.append(solver.to_physical(w_hat))
-    assert torch.equal(frames[0], expected[0])
-    for got, want in zip(frames[1:], expected[1:]):
-        assert relative(got, want) < 1e-6
+    for got, want in zip(frames, expected):
+        assert torch.equal(got, want)

@@ -5,7 +5,7 @@ combinations between them (odd batch counts against each plan's transforms per w
 the persistent kernels' resident grid, flat and tall 2D shapes, pruned bounds), as a guard
 against a case that none of them names. The radio callers and the Navier-Stokes many-step launch
 (random grid, field count across several workgroups per compute unit, step count, shared or
-per-field viscosity; against step() repeated) get samples of their own. Every sample is drawn
+per-field viscosity; against a stage per launch) get samples of their own. Every sample is drawn
 once at collection from a fixed seed, so every run checks the same cases, each under its own
 test id."""
 
@@ -261,6 +261,7 @@ FLOW_CASES = _draw_flow_cases()
                          ids=[f"ns{n}-b{b}-s{k}-{'shared' if sh else 'per-field'}"
                               for n, b, k, sh in FLOW_CASES])
 def test_random_flow_case_matches_the_stages(rng, case):
+    # Flow() defaults to drag 0.1, the value passed to the stage operators below.
     from spectral.flow import Flow
     from spectral.flow.gpu import GpuSolver
 
@@ -268,9 +269,12 @@ def test_random_flow_case_matches_the_stages(rng, case):
     viscosity = 2e-3 if shared else rng.uniform(1e-3, 5e-3, batch)
     solver = GpuSolver(n, Flow(viscosity=viscosity), 2.5e-3, pruned=True, fused=True)
     w = solver.to_spectral(dev(random_real(rng, (batch, n, n))))
-    expected = w
+    expected = w  # a stage per launch
     for _ in range(steps):
-        expected = solver.step(expected)
+        f0, predicted = torch.ops.spectral.ns_predict(expected, solver.forcing_hat, solver.nu,
+                                                      0.1, 2.5e-3, n)
+        expected = torch.ops.spectral.ns_correct(predicted, expected, f0, solver.forcing_hat,
+                                                 solver.nu, 0.1, 2.5e-3, n)
     got = solver.advance(w, steps)
     if steps == 0:
         assert torch.equal(got, w)
