@@ -53,7 +53,8 @@ constexpr double kUnstableSpread = 0.05;  // max / min - 1 above this gets a war
 const char* const kUsage =
     "usage: spectral_bench [options]\n"
     "  --op NAME         all (default), fft_c2c, fft_r2c, fft_c2r, fft2_c2c, fft2_r2c,\n"
-    "                    fft2_c2r, rfft2_modes, irfft2_modes, scale, or ns_step\n"
+    "                    fft2_c2r, rfft2_modes, irfft2_modes, scale, or ns_step (two rows:\n"
+    "                    a step as two stage launches, and 40 steps per launch, ns_steps40)\n"
     "  --impl LIST       all (default), or a comma-separated list of rocfft, ours (the scale\n"
     "                    and ns_step kernels) and our FFTs\n"
     "  --sizes LIST      comma-separated transform sizes, powers of two (default: 2,4,...,4096)\n"
@@ -762,6 +763,21 @@ void bench_ns(const Options& o, Buffers& b, hipStream_t s, std::ostream& os, boo
             },
             s, o);
         write_row(os, "ns_step", "ours", c.n, c.batch, t, w, progress);
+
+        // The same steps kStepsPerLaunch to a launch (spx_ns_steps): one row per launch.
+        constexpr int kStepsPerLaunch = 40;
+        const Work w_many{w.flops * kStepsPerLaunch, w.bytes * kStepsPerLaunch};
+        const Timing t_many = time_launches(
+            [&](int k, hipStream_t st) {
+                char* const y = static_cast<char*>(b.y[k]);
+                void* const work = y;
+                void* const out = y + 2 * field * c.batch;
+                spx_check(spx_ns_steps(b.x[k], out, work, forcing.p, viscosity, 1, 0.1f, 2.5e-3f,
+                                       n, batch, kStepsPerLaunch, st),
+                          "spx_ns_steps");
+            },
+            s, o);
+        write_row(os, "ns_steps40", "ours", c.n, c.batch, t_many, w_many, progress);
     }
 }
 
